@@ -1,0 +1,210 @@
+/*
+ * litevllm_hip.h — C ABI of the MI355X (gfx950) continuous-batching hot path.
+ *
+ * One shared library, liblitevllm_hip.so, exports these entry points.  They
+ * replace the per-step tensor work of lite-vllm 0.1.0 (pure Python/torch +
+ * two Triton kernels); each declaration below cites the reference function
+ * it replaces.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer argument named *_dev is device (HBM) memory owned by the
+ *     caller.  The library never allocates device memory; scratch space is
+ *     passed in as a workspace.
+ *   - `stream` is a hipStream_t passed as void* (NULL = legacy default
+ *     stream).  All work is enqueued asynchronously on it; nothing
+ *     synchronises the host.
+ *   - Return 0 on success, a negative lv_status on failure.  lv_last_error()
+ *     returns a thread-local, NUL-terminated description of the last failure
+ *     on the calling thread.  Argument checks happen on the host before any
+ *     launch, so a failed call has enqueued nothing.
+ *   - Entry points keep no mutable global state and are safe to call from
+ *     any host thread (the reference runs engine steps on an executor thread,
+ *     litevllm/entrypoints/async_llm.py:96-116).
+ */
+#ifndef LITEVLLM_HIP_H
+#define LITEVLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of logits / q / k / v / caches. */
+typedef enum lv_dtype {
+  LV_F32 = 0,
+  LV_F16 = 1,
+  LV_BF16 = 2
+} lv_dtype;
+
+typedef enum lv_status {
+  LV_OK = 0,
+  LV_ERR_INVALID = -1,     /* bad shape, stride, alignment or pointer */
+  LV_ERR_HIP = -2,         /* a HIP runtime call or launch failed */
+  LV_ERR_WORKSPACE = -3,   /* workspace missing or too small */
+  LV_ERR_UNSUPPORTED = -4  /* valid request this build has no kernel for */
+} lv_status;
+
+/* Thread-local description of the last error on this thread ("" if none). */
+const char* lv_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int lv_abi_version(void);
+#define LV_ABI_VERSION 1
+
+/* ------------------------------------------------------------------------
+ * (1) Ragged-batch packing.
+ *
+ * Replaces ModelRunner.prepare_inputs
+ *   (reference litevllm/engine/model_runner.py:180-260, InputMetadata 84-103,
+ *    Sequence.is_prefill / num_new_tokens engine/sequence.py:95-104,
+ *    BlockTable.physical_block_ids cache/block_manager.py:76-77).
+ *
+ * One descriptor per scheduled sequence, in batch order.  For sequence i
+ * with n = num_computed, q = query_len:
+ *   tokens cu[i] .. cu[i]+q-1 of the packed batch get
+ *     position  p = n + j                                (j = 0..q-1)
+ *     input id  = token_ids[token_offset + j]            (token_index < 0)
+ *               = device_tokens[token_index]             (token_index >= 0, q == 1)
+ *     slot      = block_ids[block_offset + p / bs] * bs + p % bs
+ *                 if p / bs < num_blocks, else 0          (model_runner.py:210-215)
+ *   cu_seqlens[i] = sum of query_len over sequences < i, cu_seqlens[B] = T
+ *   seq_start[i]  = n
+ *   context_lens[i] = n + q
+ *   block_tables[i, :] = block_ids[block_offset .. +num_blocks], padded
+ *                        with 0 to max_blocks              (model_runner.py:243-247)
+ * A reference decode sequence is n = total_len - 1, q = 1; a reference
+ * prefill is n = num_computed_tokens, q = prompt_len - n.
+ * num_seqs <= 8192.  The descriptors live in device memory, so the host
+ * cannot check them: a descriptor that points outside block_ids /
+ * token_ids / device_tokens (sizes given) yields 0 in the affected entries
+ * instead of an out-of-bounds read.  Callers validate descriptors on the
+ * host before uploading them.
+ */
+typedef struct lv_seq_desc {
+  int32_t num_computed;  /* tokens of this sequence already in the KV cache */
+  int32_t query_len;     /* tokens fed this step (>= 1)                      */
+  int32_t num_blocks;    /* length of this sequence's block table           */
+  int32_t block_offset;  /* start of its block table inside block_ids       */
+  int32_t token_offset;  /* start of its input ids inside token_ids         */
+  int32_t token_index;   /* >= 0: single input id read from device_tokens   */
+} lv_seq_desc;
+
+int lv_pack_inputs(const lv_seq_desc* descs_dev, int32_t num_seqs,
+                   const int32_t* block_ids_dev,      /* flat block tables   */
+                   int64_t num_block_ids,
+                   const int64_t* token_ids_dev,      /* flat host-fed ids   */
+                   int64_t num_token_ids,
+                   const int64_t* device_tokens_dev,  /* may be NULL         */
+                   int64_t num_device_tokens,
+                   int64_t num_tokens,                /* T = sum query_len   */
+                   int32_t block_size, int32_t max_blocks,
+                   int64_t* input_ids_dev,            /* [T]                 */
+                   int64_t* positions_dev,            /* [T]                 */
+                   int64_t* slot_mapping_dev,         /* [T]                 */
+                   int32_t* cu_seqlens_dev,           /* [B+1]               */
+                   int32_t* seq_start_dev,            /* [B]                 */
+                   int32_t* context_lens_dev,         /* [B]                 */
+                   int32_t* block_tables_dev,         /* [B, max_blocks]     */
+                   void* stream);
+
+/* ------------------------------------------------------------------------
+ * (2) KV-cache scatter keyed by slot_mapping.
+ *
+ * Replaces the inline scatter in Attention.forward
+ *   (reference litevllm/layers/attention.py:79-84) and
+ *   PagedAttention.write_to_cache (attention.py:17-33):
+ *     key_cache[slot / bs, slot % bs, :, :] = key[t]   (same for value)
+ * key/value: [T, num_kv_heads, head_dim] with token stride *_stride_t
+ * (elements), heads contiguous.  Caches: contiguous
+ * [num_blocks, block_size, num_kv_heads, head_dim].  Slots < 0 are skipped
+ * (padding); slots >= num_blocks*block_size are skipped so no write leaves
+ * the cache.  Duplicate slots in one call: last writer undefined (torch's
+ * index_put is undefined there too).
+ */
+int lv_kv_scatter(const void* key_dev, int64_t key_stride_t,
+                  const void* value_dev, int64_t value_stride_t,
+                  void* key_cache_dev, void* value_cache_dev,
+                  const int64_t* slot_mapping_dev, int64_t num_tokens,
+                  int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                  int64_t num_blocks, lv_dtype dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * (3) Paged attention over a mixed batch.
+ *
+ * Replaces Attention._decode_fast (reference litevllm/layers/attention.py:
+ * 91-139) for 1-token decodes and Attention._prefill (attention.py:141-151)
+ * for prefill chunks, extended to chunks that start at an offset and read
+ * the cached prefix from the paged cache.
+ *
+ * Sequence i owns query rows cu_seqlens[i] .. cu_seqlens[i+1]-1 and has
+ * context_lens[i] tokens in the cache (including this step's tokens, which
+ * must already be scattered).  Query row j of sequence i sits at position
+ * p = context_lens[i] - q_i + j and attends keys 0..p (causal; for a decode
+ * this is the reference mask pos < context_len, attention.py:132).  Query
+ * head h reads kv head h / (num_heads / num_kv_heads) (attention.py:124).
+ * Softmax is taken in fp32 of (q.k) * scale; out is written in `dtype`.
+ *
+ * The first num_decodes sequences must have exactly one query row each
+ * (decode); the rest are prefill chunks of any length <= max_query_len.
+ * cu_seqlens_dev may be NULL when num_decodes == num_seqs (row i = seq i).
+ * query: [T, num_heads, head_dim], token stride q_stride_t; out likewise
+ * with out_stride_t.  Caches as in lv_kv_scatter.  block_tables:
+ * [num_seqs, max_blocks] int32.
+ * num_cache_blocks bounds every block id read from block_tables (an id
+ * outside [0, num_cache_blocks) reads block 0 instead of faulting); context
+ * lengths are clamped to max_blocks * block_size.
+ * workspace: at least lv_paged_attention_workspace_size(...) bytes, 256-B
+ * aligned; contents need not be initialised.
+ * Supported: head_dim 64 or 128, block_size 16, num_heads / num_kv_heads in
+ * {1, 2, 4, 8}; anything else returns LV_ERR_UNSUPPORTED.
+ */
+size_t lv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_decodes,
+                                         int64_t num_tokens, int32_t num_heads,
+                                         int32_t head_dim, int32_t block_size,
+                                         int32_t max_blocks, int32_t max_query_len,
+                                         lv_dtype dtype);
+
+int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
+                       const void* key_cache_dev, const void* value_cache_dev,
+                       int64_t num_cache_blocks,
+                       const int32_t* block_tables_dev, int32_t max_blocks,
+                       const int32_t* cu_seqlens_dev,
+                       const int32_t* context_lens_dev,
+                       int32_t num_seqs, int32_t num_decodes, int64_t num_tokens,
+                       int32_t max_query_len,
+                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int32_t block_size, float scale,
+                       void* out_dev, int64_t out_stride_t,
+                       void* workspace_dev, size_t workspace_bytes,
+                       lv_dtype dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * (4) Fused greedy / temperature sampler.
+ *
+ * Replaces Sampler.sample's greedy branch (_triton_argmax / _argmax_kernel,
+ * reference litevllm/layers/sampler.py:60-84, 111-124, 175-176) and its
+ * temperature branch without top-k/top-p (_triton_softmax_temp +
+ * torch.multinomial, sampler.py:86-108, 127-144, 177-187).
+ *
+ * Row r of logits [B, V] (row stride row_stride elements):
+ *   temperature[r] == 0 : out[r] = first index of the fp32 maximum.
+ *   temperature[r] >  0 : out[r] = inverse-CDF draw of softmax(x / T) at the
+ *                         caller-supplied uniform[r] in [0, 1), with the
+ *                         fixed-order fp32 arithmetic defined in sampler.hip
+ *                         (bit-reproducible; the CPU restatement matches it
+ *                         bit for bit).
+ * temperature_dev / uniform_dev: fp32 [B]; uniform may be NULL if every row
+ * is greedy.  out_ids_dev: int64 [B].
+ */
+int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
+              int64_t row_stride, const float* temperature_dev,
+              const float* uniform_dev, int64_t* out_ids_dev, lv_dtype dtype,
+              void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LITEVLLM_HIP_H */

@@ -1,0 +1,333 @@
+// Fused greedy / temperature sampler over [B, V] logits, one workgroup per
+// row.
+//
+// Greedy rows (temperature 0) follow _argmax_kernel / torch.argmax
+// (reference litevllm/layers/sampler.py:60-84, 111-124): the first index of
+// the fp32 maximum.  NaN entries never win; a row with no finite-or-+inf
+// maximum (all -inf / NaN) returns 0.
+//
+// Temperature rows replace softmax(x / T) + torch.multinomial
+// (sampler.py:127-144, 177-187) by an inverse-CDF draw at a caller-supplied
+// uniform u in [0, 1).  The arithmetic is fixed so that the CPU
+// restatement reproduces it bit for bit:
+//
+//   c      = log2(e) / T                       (one correctly rounded division)
+//   segment s = elements [512 s, 512 s + 512)  (last one partial)
+//   m_s    = max of the segment, e_j = exp2_det((x_j - m_s) * c)
+//   a_k    = e_{8k} + ... + e_{8k+7}  sequentially, lane chunk k = 0..63
+//   A_k    = inclusive Hillis-Steele scan of a_k over k (step d = 1..32:
+//            A_k <- A_k + A_{k-d} for k >= d, all k at once)
+//   sigma_s = A_63
+//   M      = max_s m_s,  w_s = sigma_s * exp2_det((m_s - M) * c)
+//   R      = ceil(nseg / 64); group k holds segments [kR, kR + R)
+//   b_k    = w_{kR} + w_{kR+1} + ... sequentially; B_k = Hillis-Steele scan
+//   S = B_63, r = u * S
+//   level 1: k* = first k with B_k > r and b_k > 0, else last k with b_k > 0
+//   level 2: acc = B_{k*-1} (0 for k* = 0); walk segments of k* in order,
+//            first s with (acc + w_s) > r, else the last s with w_s > 0
+//            (acc advanced sequentially: acc <- acc + w_s); base = acc
+//            before s
+//   level 3: scale = exp2_det((m_s - M) * c); first lane chunk k with
+//            base + A_k * scale > r and a_k > 0, else last k with a_k > 0
+//   level 4: q = A_{k-1} (0 for k = 0); for j in the chunk: q <- q + e_j;
+//            first j with e_j > 0 and base + q * scale > r, else the last j
+//            with e_j > 0.
+// Every sum, product and comparison is an IEEE fp32 operation in the order
+// written (this file is compiled with -ffp-contract=off); exp2_det uses only
+// fmaf, rint and exact power-of-two scaling.
+#include "lv_common.h"
+
+namespace lv {
+
+constexpr int kSampThreads = 1024;
+constexpr int kSampWaves = kSampThreads / 64;
+constexpr int kSeg = 512;
+constexpr int kMaxSegs = 4096;  // vocab up to 2^21
+
+// log2(e) rounded to fp32.
+constexpr float kLog2e = 0x1.715476p+0f;
+
+// exp2 for t <= 0 by range reduction t = n + f, |f| <= 1/2, and the degree-7
+// Taylor polynomial of 2^f = sum_k (f ln2)^k / k! (coefficients ln2^k/k!
+// rounded to fp32) evaluated by Horner with fused multiply-adds; 2^n is
+// applied by an exact power-of-two multiply.  Inputs below -125 (and NaN)
+// give 0, so no result is subnormal.  Relative error < 2^-22 on [-125, 0].
+__device__ __forceinline__ float exp2_det(float t) {
+  if (!(t >= -125.0f)) return 0.0f;
+  if (t > 0.0f) t = 0.0f;
+  const float n = rintf(t);
+  const float f = t - n;  // exact (Sterbenz)
+  float p = 0x1.ffcbfcp-17f;
+  p = fmaf(p, f, 0x1.430912p-13f);
+  p = fmaf(p, f, 0x1.5d87fep-10f);
+  p = fmaf(p, f, 0x1.3b2ab6p-7f);
+  p = fmaf(p, f, 0x1.c6b08ep-5f);
+  p = fmaf(p, f, 0x1.ebfbep-3f);
+  p = fmaf(p, f, 0x1.62e43p-1f);
+  p = fmaf(p, f, 1.0f);
+  const int ni = (int)n;
+  const float scale = __uint_as_float((uint32_t)(ni + 127) << 23);
+  return p * scale;
+}
+
+// Load elements [512 s + 8 lane, +8) of a row as fp32; entries past V are
+// -inf.  `vec` says the row start is 16-byte aligned.
+template <typename T>
+__device__ __forceinline__ void load_chunk(const T* __restrict__ row, int64_t V, int s, int lane,
+                                           bool vec, float x[8]) {
+  const int64_t e0 = (int64_t)s * kSeg + lane * 8;
+  if (vec && e0 + 8 <= V) {
+    if constexpr (elem<T>::kPer16B == 8) {
+      elem<T>::unpack(load16(row + e0), x);
+    } else {
+      elem<T>::unpack(load16(row + e0), x);
+      elem<T>::unpack(load16(row + e0 + 4), x + 4);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      x[j] = (e0 + j < V) ? elem<T>::load(row + e0 + j) : -__builtin_inff();
+  }
+}
+
+// Inclusive Hillis-Steele scan across the 64 lanes of a wavefront.
+__device__ __forceinline__ float wave_scan_hs(float a, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float y = __shfl_up(a, d);
+    if (lane >= d) a = a + y;
+  }
+  return a;
+}
+
+// Per-chunk exp weights and their sequential sum (the a_k of the header).
+__device__ __forceinline__ float chunk_weights(const float x[8], float ms, float c, float e[8]) {
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    e[j] = exp2_det((x[j] - ms) * c);
+    a = a + e[j];
+  }
+  return a;
+}
+
+__device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSampThreads) void sampler_kernel(
+    const T* __restrict__ logits, int64_t V, int64_t row_stride,
+    const float* __restrict__ temperature, const float* __restrict__ uniform,
+    int64_t* __restrict__ out, int vec_ok) {
+  __shared__ float s_m[kMaxSegs];
+  __shared__ float s_w[kMaxSegs];
+  __shared__ float s_gv[kSampWaves];
+  __shared__ int64_t s_gi[kSampWaves];
+
+  const int64_t r = blockIdx.x;
+  const T* row = logits + r * row_stride;
+  const int nseg = (int)((V + kSeg - 1) / kSeg);
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const bool vec = vec_ok != 0;
+
+  const float temp = temperature[r];
+  const float c = kLog2e / temp;
+  const bool greedy = !(temp > 0.0f) || !(c <= 3.0e38f);
+
+  if (greedy) {
+    float bv = -__builtin_inff();
+    int64_t bi = INT64_MAX;
+    for (int s = wave; s < nseg; s += 2 * kSampWaves) {
+      float x0[8], x1[8];
+      const int s1 = s + kSampWaves;
+      load_chunk(row, V, s, lane, vec, x0);
+      if (s1 < nseg) load_chunk(row, V, s1, lane, vec, x1);
+      const int64_t e0 = (int64_t)s * kSeg + lane * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (x0[j] > bv) { bv = x0[j]; bi = e0 + j; }
+      if (s1 < nseg) {
+        const int64_t e1 = (int64_t)s1 * kSeg + lane * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (x1[j] > bv) { bv = x1[j]; bi = e1 + j; }
+      }
+    }
+    // Lanes may hold their best from a later segment than an equal value of
+    // another lane, so the merge is lexicographic on (value, index).
+#pragma unroll
+    for (int ofs = 32; ofs >= 1; ofs >>= 1) {
+      const float ov = __shfl_xor(bv, ofs);
+      const int64_t oi = __shfl_xor(bi, ofs);
+      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { s_gv[wave] = bv; s_gi[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < kSampWaves; ++w)
+        if (better(s_gv[w], s_gi[w], bv, bi)) { bv = s_gv[w]; bi = s_gi[w]; }
+      out[r] = (bi == INT64_MAX) ? 0 : bi;
+    }
+    return;
+  }
+
+  // Phase 1: per-segment max and scanned exp weights.
+  for (int s = wave; s < nseg; s += 2 * kSampWaves) {
+    float x0[8], x1[8], e[8];
+    const int s1 = s + kSampWaves;
+    load_chunk(row, V, s, lane, vec, x0);
+    if (s1 < nseg) load_chunk(row, V, s1, lane, vec, x1);
+    {
+      float ms = x0[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) ms = fmaxf(ms, x0[j]);
+      ms = group_max<64>(ms);
+      const float A = wave_scan_hs(chunk_weights(x0, ms, c, e), lane);
+      if (lane == 63) { s_m[s] = ms; s_w[s] = A; }
+    }
+    if (s1 < nseg) {
+      float ms = x1[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) ms = fmaxf(ms, x1[j]);
+      ms = group_max<64>(ms);
+      const float A = wave_scan_hs(chunk_weights(x1, ms, c, e), lane);
+      if (lane == 63) { s_m[s1] = ms; s_w[s1] = A; }
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // Phase 2 (one wavefront): segment weights, total and the search.
+  float M = -__builtin_inff();
+  for (int s = lane; s < nseg; s += 64) M = fmaxf(M, s_m[s]);
+  M = group_max<64>(M);
+  const int R = (nseg + 63) / 64;
+  const int g0 = min(nseg, lane * R), g1 = min(nseg, g0 + R);
+  float b = 0.0f;
+  for (int s = g0; s < g1; ++s) {
+    const float w = s_w[s] * exp2_det((s_m[s] - M) * c);
+    s_w[s] = w;  // each lane owns its own segments
+    b = b + w;
+  }
+  const float B = wave_scan_hs(b, lane);
+  const float S = __shfl(B, 63);
+  if (!(S > 0.0f)) {
+    if (lane == 0) out[r] = 0;
+    return;
+  }
+  const float u = uniform[r];
+  const float target = u * S;
+
+  // Level 1.
+  const uint64_t hit = __ballot(B > target && b > 0.0f);
+  int k;
+  if (hit) {
+    k = __ffsll((unsigned long long)hit) - 1;
+  } else {
+    const uint64_t nz = __ballot(b > 0.0f);
+    k = 63 - __clzll((long long)nz);
+  }
+  const float Bprev = __shfl(B, k > 0 ? k - 1 : 0);
+  const float base_k = (k == 0) ? 0.0f : Bprev;
+
+  // Level 2 (uniform across lanes: every lane walks the same segments).
+  const int t0 = min(nseg, k * R), t1 = min(nseg, t0 + R);
+  int sstar = -1;
+  float base = 0.0f;
+  {
+    float acc = base_k;
+    for (int s = t0; s < t1; ++s) {
+      const float w = s_w[s];
+      const float nxt = acc + w;
+      if (nxt > target) { sstar = s; base = acc; break; }
+      acc = nxt;
+    }
+    if (sstar < 0) {
+      acc = base_k;
+      for (int s = t0; s < t1; ++s) {
+        const float w = s_w[s];
+        if (w > 0.0f) { sstar = s; base = acc; }
+        acc = acc + w;
+      }
+    }
+  }
+
+  // Unreachable when S > 0 (group k* holds a positive weight); kept so a
+  // logic error can never turn into an out-of-bounds read.
+  if (sstar < 0) sstar = 0;
+
+  // Level 3: recompute the segment's chunk weights exactly as in phase 1.
+  float x[8], e[8];
+  load_chunk(row, V, sstar, lane, vec, x);
+  float ms = x[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) ms = fmaxf(ms, x[j]);
+  ms = group_max<64>(ms);
+  const float a = chunk_weights(x, ms, c, e);
+  const float A = wave_scan_hs(a, lane);
+  const float Aprev = __shfl_up(A, 1);
+  const float scale = exp2_det((s_m[sstar] - M) * c);
+  const uint64_t hit3 = __ballot((base + A * scale > target) && a > 0.0f);
+  int kk;
+  if (hit3) {
+    kk = __ffsll((unsigned long long)hit3) - 1;
+  } else {
+    const uint64_t nz = __ballot(a > 0.0f);
+    kk = nz ? 63 - __clzll((long long)nz) : 0;
+  }
+
+  // Level 4.
+  if (lane == kk) {
+    float q = (kk == 0) ? 0.0f : Aprev;
+    int jstar = -1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      q = q + e[j];
+      if (jstar < 0 && e[j] > 0.0f && base + q * scale > target) jstar = j;
+    }
+    if (jstar < 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (e[j] > 0.0f) jstar = j;
+    }
+    if (jstar < 0) jstar = 0;
+    out[r] = (int64_t)sstar * kSeg + kk * 8 + jstar;
+  }
+}
+
+}  // namespace lv
+
+extern "C" int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
+                         int64_t row_stride, const float* temperature_dev, const float* uniform_dev,
+                         int64_t* out_ids_dev, lv_dtype dtype, void* stream) {
+  using namespace lv;
+  clear_error();
+  LV_REQUIRE(dtype == LV_F32 || dtype == LV_F16 || dtype == LV_BF16, "lv_sample: bad dtype");
+  LV_REQUIRE(num_rows >= 0 && num_rows <= 0x7fffffff, "lv_sample: bad num_rows");
+  if (num_rows == 0) return LV_OK;
+  LV_REQUIRE(vocab_size >= 1 && vocab_size <= (int64_t)kSeg * kMaxSegs,
+             "lv_sample: vocab_size=%lld outside [1, %d]", (long long)vocab_size, kSeg * kMaxSegs);
+  LV_REQUIRE(row_stride >= vocab_size, "lv_sample: row_stride < vocab_size");
+  LV_REQUIRE(logits_dev && temperature_dev && out_ids_dev, "lv_sample: null pointer");
+  LV_REQUIRE(uniform_dev, "lv_sample: uniform draws required (pass zeros for all-greedy rows)");
+  const int vec = aligned16(logits_dev) && ((row_stride * (int64_t)dtype_size(dtype)) % 16 == 0);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)num_rows), block(kSampThreads);
+  switch (dtype) {
+    case LV_BF16:
+      hipLaunchKernelGGL(sampler_kernel<bf16>, grid, block, 0, st, (const bf16*)logits_dev,
+                         vocab_size, row_stride, temperature_dev, uniform_dev, out_ids_dev, vec);
+      break;
+    case LV_F16:
+      hipLaunchKernelGGL(sampler_kernel<f16>, grid, block, 0, st, (const f16*)logits_dev,
+                         vocab_size, row_stride, temperature_dev, uniform_dev, out_ids_dev, vec);
+      break;
+    default:
+      hipLaunchKernelGGL(sampler_kernel<float>, grid, block, 0, st, (const float*)logits_dev,
+                         vocab_size, row_stride, temperature_dev, uniform_dev, out_ids_dev, vec);
+      break;
+  }
+  return check_launch("lv_sample");
+}

@@ -1,0 +1,100 @@
+"""ctypes binding of liblitevllm_hip.so (the C ABI in include/litevllm_hip.h).
+
+The library is loaded lazily on first use.  There is no fallback: if the
+library is missing or cannot be loaded, every hot-path op raises
+``RuntimeError`` (the reference's Triton sampler silently fell back to torch,
+litevllm/layers/sampler.py:38-55; this build fails loudly instead so a GPU
+run can never pass on a non-native path).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_NAME = "liblitevllm_hip.so"
+LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
+
+LV_F32, LV_F16, LV_BF16 = 0, 1, 2
+ABI_VERSION = 1
+
+# Every symbol the header declares, with (restype, argtypes).
+_c_i32, _c_i64, _c_f32, _c_p, _c_sz = (
+    ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t)
+
+SIGNATURES: dict[str, tuple] = {
+    "lv_last_error": (ctypes.c_char_p, []),
+    "lv_abi_version": (ctypes.c_int, []),
+    "lv_pack_inputs": (ctypes.c_int, [
+        _c_p, _c_i32,            # descs, num_seqs
+        _c_p, _c_i64,            # block_ids, num_block_ids
+        _c_p, _c_i64,            # token_ids, num_token_ids
+        _c_p, _c_i64,            # device_tokens, num_device_tokens
+        _c_i64, _c_i32, _c_i32,  # num_tokens, block_size, max_blocks
+        _c_p, _c_p, _c_p,        # input_ids, positions, slot_mapping
+        _c_p, _c_p, _c_p, _c_p,  # cu_seqlens, seq_start, context_lens, block_tables
+        _c_p,                    # stream
+    ]),
+    "lv_kv_scatter": (ctypes.c_int, [
+        _c_p, _c_i64, _c_p, _c_i64,   # key, key_stride_t, value, value_stride_t
+        _c_p, _c_p,                   # key_cache, value_cache
+        _c_p, _c_i64,                 # slot_mapping, num_tokens
+        _c_i32, _c_i32, _c_i32,       # num_kv_heads, head_dim, block_size
+        _c_i64, ctypes.c_int, _c_p,   # num_blocks, dtype, stream
+    ]),
+    "lv_paged_attention_workspace_size": (_c_sz, [
+        _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_int,
+    ]),
+    "lv_paged_attention": (ctypes.c_int, [
+        _c_p, _c_i64,                 # query, q_stride_t
+        _c_p, _c_p, _c_i64,           # key_cache, value_cache, num_cache_blocks
+        _c_p, _c_i32,                 # block_tables, max_blocks
+        _c_p, _c_p,                   # cu_seqlens, context_lens
+        _c_i32, _c_i32, _c_i64,       # num_seqs, num_decodes, num_tokens
+        _c_i32,                       # max_query_len
+        _c_i32, _c_i32, _c_i32,       # num_heads, num_kv_heads, head_dim
+        _c_i32, _c_f32,               # block_size, scale
+        _c_p, _c_i64,                 # out, out_stride_t
+        _c_p, _c_sz,                  # workspace, workspace_bytes
+        ctypes.c_int, _c_p,           # dtype, stream
+    ]),
+    "lv_sample": (ctypes.c_int, [
+        _c_p, _c_i64, _c_i64, _c_i64,  # logits, num_rows, vocab_size, row_stride
+        _c_p, _c_p, _c_p,              # temperature, uniform, out_ids
+        ctypes.c_int, _c_p,            # dtype, stream
+    ]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load and bind the library (once per process); raise if unavailable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_NAME} is not built (expected at {LIB_PATH}); build it with "
+                "`python -m litevllm._build` or __graft_entry__.build()")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)  # AttributeError if a symbol is missing
+            fn.restype = restype
+            fn.argtypes = argtypes
+        v = lib.lv_abi_version()
+        if v != ABI_VERSION:
+            raise RuntimeError(f"{LIB_NAME} ABI version {v} != expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().lv_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")

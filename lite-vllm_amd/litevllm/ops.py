@@ -1,0 +1,276 @@
+"""Tensor-level wrappers of the HIP hot path (one function per C entry point).
+
+Each wrapper checks shapes, dtypes and devices on the host, passes raw
+pointers plus the current HIP stream to liblitevllm_hip.so, and raises
+``RuntimeError`` with the library's message on failure.  Inputs must be
+tensors on a ROCm ("cuda") device: there is no CPU path behind these calls.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _hip
+
+_DTYPE_CODES = {
+    torch.float32: _hip.LV_F32,
+    torch.float16: _hip.LV_F16,
+    torch.bfloat16: _hip.LV_BF16,
+}
+
+# Field order of lv_seq_desc (include/litevllm_hip.h).
+SEQ_DESC_FIELDS = ("num_computed", "query_len", "num_blocks", "block_offset",
+                   "token_offset", "token_index")
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise RuntimeError(f"unsupported dtype {t.dtype}; expected fp32, fp16 or bf16") from None
+
+
+def _require_device(name: str, t: Optional[torch.Tensor], device: torch.device) -> None:
+    if t is None:
+        return
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"litevllm HIP op: `{name}` is on {t.device}; the hot path runs only on a "
+            "ROCm device (there is no CPU implementation)")
+    if t.device != device:
+        raise RuntimeError(f"litevllm HIP op: `{name}` on {t.device}, expected {device}")
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_int(name: str, t: torch.Tensor, dtype: torch.dtype, dim: int) -> None:
+    if t.dtype != dtype or t.dim() != dim or not t.is_contiguous():
+        raise RuntimeError(f"`{name}` must be a contiguous {dim}-d {dtype} tensor, "
+                           f"got {t.dtype} {tuple(t.shape)} contiguous={t.is_contiguous()}")
+
+
+# ---------------------------------------------------------------------------
+# (2) KV scatter
+# ---------------------------------------------------------------------------
+
+def kv_scatter(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+               value_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """key_cache[slot // bs, slot % bs] = key (same for value), in place.
+
+    Reference: litevllm/layers/attention.py:17-33 and 79-84.
+    key/value: [T, Hkv, D] (token stride free, heads contiguous);
+    caches: contiguous [N, bs, Hkv, D]; slot_mapping: int64 [T].
+    """
+    dev = key_cache.device
+    for n, t in (("key", key), ("value", value), ("key_cache", key_cache),
+                 ("value_cache", value_cache), ("slot_mapping", slot_mapping)):
+        _require_device(n, t, dev)
+    if key_cache.dim() != 4 or not key_cache.is_contiguous() or not value_cache.is_contiguous():
+        raise RuntimeError("caches must be contiguous [num_blocks, block_size, num_kv_heads, head_dim]")
+    if value_cache.shape != key_cache.shape:
+        raise RuntimeError("key_cache and value_cache shapes differ")
+    n_blocks, bs, hkv, d = key_cache.shape
+    T = slot_mapping.shape[0]
+    _check_int("slot_mapping", slot_mapping, torch.int64, 1)
+    for n, t in (("key", key), ("value", value)):
+        if tuple(t.shape) != (T, hkv, d):
+            raise RuntimeError(f"`{n}` shape {tuple(t.shape)} != {(T, hkv, d)}")
+        if t.dtype != key_cache.dtype:
+            raise RuntimeError(f"`{n}` dtype {t.dtype} != cache dtype {key_cache.dtype}")
+        if T > 0 and (t.stride(2) != 1 or t.stride(1) != d):
+            raise RuntimeError(f"`{n}` must have contiguous heads (strides {t.stride()})")
+    if T == 0:
+        return
+    lib = _hip.load()
+    rc = lib.lv_kv_scatter(_ptr(key), key.stride(0), _ptr(value), value.stride(0),
+                           _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping), T,
+                           hkv, d, bs, n_blocks, _dtype_code(key_cache), _stream(dev))
+    _hip.check(rc, "lv_kv_scatter")
+
+
+# ---------------------------------------------------------------------------
+# (3) paged attention
+# ---------------------------------------------------------------------------
+
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> Optional[torch.Tensor]:
+    """Per-(device, stream) scratch buffer, grown on demand and reused."""
+    if nbytes == 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           _stream(device))
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                    block_tables: torch.Tensor, context_lens: torch.Tensor, *,
+                    num_kv_heads: Optional[int] = None, scale: float,
+                    cu_seqlens: Optional[torch.Tensor] = None,
+                    num_decodes: Optional[int] = None, max_query_len: int = 1,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention of every query row over its sequence's paged K/V.
+
+    Reference: litevllm/layers/attention.py:91-139 (decode) and 141-151
+    (prefill, here generalised to chunks at an offset).  query: [T, H, D];
+    block_tables int32 [B, max_blocks]; context_lens int32 [B] (tokens in
+    cache incl. this step's); cu_seqlens int32 [B+1] (None => T == B, all
+    decodes); the first ``num_decodes`` sequences must be 1-token decodes.
+    """
+    dev = key_cache.device
+    for n, t in (("query", query), ("key_cache", key_cache), ("value_cache", value_cache),
+                 ("block_tables", block_tables), ("context_lens", context_lens),
+                 ("cu_seqlens", cu_seqlens), ("out", out)):
+        _require_device(n, t, dev)
+    if query.dim() != 3 or query.stride(2) != 1 or query.stride(1) != query.shape[2]:
+        raise RuntimeError(f"query must be [T, H, D] with contiguous heads, got "
+                           f"{tuple(query.shape)} strides {query.stride()}")
+    T, H, D = query.shape
+    n_blocks, bs, hkv, d = key_cache.shape
+    if num_kv_heads is not None and num_kv_heads != hkv:
+        raise RuntimeError(f"num_kv_heads={num_kv_heads} but cache has {hkv}")
+    if d != D or value_cache.shape != key_cache.shape:
+        raise RuntimeError("cache head_dim / shapes do not match the query")
+    if query.dtype != key_cache.dtype or value_cache.dtype != key_cache.dtype:
+        raise RuntimeError("query and caches must share one dtype")
+    if not key_cache.is_contiguous() or not value_cache.is_contiguous():
+        raise RuntimeError("caches must be contiguous")
+    _check_int("block_tables", block_tables, torch.int32, 2)
+    _check_int("context_lens", context_lens, torch.int32, 1)
+    B, max_blocks = block_tables.shape
+    if context_lens.shape[0] != B:
+        raise RuntimeError("context_lens and block_tables disagree on the batch size")
+    if cu_seqlens is None:
+        if T != B:
+            raise RuntimeError("without cu_seqlens every sequence must have exactly one query row")
+        num_decodes = B if num_decodes is None else num_decodes
+    else:
+        _check_int("cu_seqlens", cu_seqlens, torch.int32, 1)
+        if cu_seqlens.shape[0] != B + 1:
+            raise RuntimeError("cu_seqlens must have num_seqs + 1 entries")
+        num_decodes = 0 if num_decodes is None else num_decodes
+    if out is None:
+        out = torch.empty_like(query, memory_format=torch.contiguous_format)
+    elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1 \
+            or out.stride(1) != D:
+        raise RuntimeError("`out` must match query's shape/dtype with contiguous heads")
+    if B == 0:
+        return out
+    lib = _hip.load()
+    dt = _dtype_code(query)
+    ws_bytes = lib.lv_paged_attention_workspace_size(B, num_decodes, T, H, D, bs, max_blocks,
+                                                     max_query_len, dt)
+    ws = _workspace(dev, ws_bytes)
+    rc = lib.lv_paged_attention(
+        _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache), n_blocks,
+        _ptr(block_tables), max_blocks, _ptr(cu_seqlens), _ptr(context_lens),
+        B, num_decodes, T, max_query_len, H, hkv, D, bs, float(scale),
+        _ptr(out), out.stride(0), _ptr(ws), 0 if ws is None else ws.numel(), dt, _stream(dev))
+    _hip.check(rc, "lv_paged_attention")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# (1) packing
+# ---------------------------------------------------------------------------
+
+def pack_inputs(descs: torch.Tensor, block_ids: torch.Tensor, token_ids: torch.Tensor,
+                num_tokens: int, block_size: int, max_blocks: int,
+                device_tokens: Optional[torch.Tensor] = None) -> dict[str, torch.Tensor]:
+    """Expand per-sequence descriptors into the packed step tensors on the GPU.
+
+    Reference: ModelRunner.prepare_inputs, litevllm/engine/model_runner.py:180-260.
+    descs: int32 [B, 6] device tensor in lv_seq_desc field order
+    (SEQ_DESC_FIELDS); block_ids int32 [*]; token_ids int64 [*];
+    device_tokens int64 [*] or None.
+    Returns input_ids/positions/slot_mapping (int64 [T]), cu_seqlens
+    (int32 [B+1]), seq_start/context_lens (int32 [B]) and block_tables
+    (int32 [B, max_blocks]).
+    """
+    dev = descs.device
+    for n, t in (("descs", descs), ("block_ids", block_ids), ("token_ids", token_ids),
+                 ("device_tokens", device_tokens)):
+        _require_device(n, t, dev)
+    _check_int("descs", descs, torch.int32, 2)
+    if descs.shape[1] != len(SEQ_DESC_FIELDS):
+        raise RuntimeError("descs must be [B, 6] int32")
+    _check_int("block_ids", block_ids, torch.int32, 1)
+    _check_int("token_ids", token_ids, torch.int64, 1)
+    if device_tokens is not None:
+        _check_int("device_tokens", device_tokens, torch.int64, 1)
+    B = descs.shape[0]
+    T = int(num_tokens)
+    out = {
+        "input_ids": torch.empty(T, dtype=torch.int64, device=dev),
+        "positions": torch.empty(T, dtype=torch.int64, device=dev),
+        "slot_mapping": torch.empty(T, dtype=torch.int64, device=dev),
+        "cu_seqlens": torch.empty(B + 1, dtype=torch.int32, device=dev),
+        "seq_start": torch.empty(B, dtype=torch.int32, device=dev),
+        "context_lens": torch.empty(B, dtype=torch.int32, device=dev),
+        "block_tables": torch.empty((B, max_blocks), dtype=torch.int32, device=dev),
+    }
+    lib = _hip.load()
+    rc = lib.lv_pack_inputs(
+        _ptr(descs), B, _ptr(block_ids), block_ids.numel(), _ptr(token_ids), token_ids.numel(),
+        _ptr(device_tokens), 0 if device_tokens is None else device_tokens.numel(),
+        T, block_size, max_blocks,
+        _ptr(out["input_ids"]), _ptr(out["positions"]), _ptr(out["slot_mapping"]),
+        _ptr(out["cu_seqlens"]), _ptr(out["seq_start"]), _ptr(out["context_lens"]),
+        _ptr(out["block_tables"]), _stream(dev))
+    _hip.check(rc, "lv_pack_inputs")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# (4) sampler
+# ---------------------------------------------------------------------------
+
+def sample(logits: torch.Tensor, temperature: torch.Tensor,
+           uniform: Optional[torch.Tensor] = None,
+           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Greedy (temperature 0) or inverse-CDF temperature sampling per row.
+
+    Reference: litevllm/layers/sampler.py:60-187.  logits [B, V] (unit
+    stride along V); temperature / uniform: float32 [B] (uniform in [0, 1),
+    may be None when every row is greedy).  Returns int64 [B].
+    """
+    dev = logits.device
+    for n, t in (("logits", logits), ("temperature", temperature), ("uniform", uniform),
+                 ("out", out)):
+        _require_device(n, t, dev)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise RuntimeError("logits must be [B, V] with unit stride along V")
+    B, V = logits.shape
+    _check_int("temperature", temperature, torch.float32, 1)
+    if temperature.shape[0] != B:
+        raise RuntimeError("temperature must have one entry per row")
+    if uniform is None:
+        uniform = torch.zeros(B, dtype=torch.float32, device=dev)
+    _check_int("uniform", uniform, torch.float32, 1)
+    if uniform.shape[0] != B:
+        raise RuntimeError("uniform must have one entry per row")
+    if out is None:
+        out = torch.empty(B, dtype=torch.int64, device=dev)
+    else:
+        _check_int("out", out, torch.int64, 1)
+    if B == 0:
+        return out
+    lib = _hip.load()
+    rc = lib.lv_sample(_ptr(logits), B, V, logits.stride(0), _ptr(temperature), _ptr(uniform),
+                       _ptr(out), _dtype_code(logits), _stream(dev))
+    _hip.check(rc, "lv_sample")
+    return out

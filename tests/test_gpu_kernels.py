@@ -1,0 +1,279 @@
+"""GPU parity of the four hot-path kernels against the CPU oracle.
+
+Bars: packing, slot_mapping and KV scatter bit-exact; greedy argmax
+bit-exact; temperature sampling bit-exact against oracle/sampler_ref.c at
+the same uniforms; attention within 2e-2 max-abs and 1e-3 mean-abs of the
+fp32 oracle on the same bf16 inputs (plus relative L2 <= 1e-2).
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from litevllm import ops, workloads
+from oracle import attention as oatt
+from oracle import packing as opack
+from oracle import sampler as osamp
+from oracle import scatter as oscat
+
+pytestmark = pytest.mark.gpu
+
+ATOL_MAX, ATOL_MEAN, REL_L2 = 2e-2, 1e-3, 1e-2
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _check_attention(got: torch.Tensor, ref: torch.Tensor, what: str):
+    got = got.float().cpu()
+    err = (got - ref).abs()
+    rel = (got - ref).norm() / ref.norm().clamp_min(1e-30)
+    assert torch.isfinite(got).all(), f"{what}: non-finite output"
+    assert err.max() <= ATOL_MAX, f"{what}: max-abs {err.max():.3e}"
+    assert err.mean() <= ATOL_MEAN, f"{what}: mean-abs {err.mean():.3e}"
+    assert rel <= REL_L2, f"{what}: rel-L2 {rel:.3e}"
+
+
+# ---------------------------------------------------------------------------
+# KV scatter
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("strided", [False, True])
+def test_kv_scatter_bit_exact(device, dtype, strided):
+    _say(f"kv_scatter dtype={dtype} strided={strided}")
+    g = torch.Generator().manual_seed(11)
+    N, bs, Hkv, D, T = 64, 16, 8, 128, 300
+    kc = torch.full((N, bs, Hkv, D), 3.5, dtype=dtype)
+    vc = torch.full((N, bs, Hkv, D), -3.5, dtype=dtype)
+    slots = torch.randperm(N * bs, generator=g)[:T].to(torch.int64)
+    slots[::37] = -1
+    if strided:
+        qkv = torch.randn(T, (16 + 2 * Hkv) * D, generator=g).to(dtype)
+        k = qkv[:, 16 * D:(16 + Hkv) * D].view(T, Hkv, D)
+        v = qkv[:, (16 + Hkv) * D:].view(T, Hkv, D)
+    else:
+        k = torch.randn(T, Hkv, D, generator=g).to(dtype)
+        v = torch.randn(T, Hkv, D, generator=g).to(dtype)
+    kc_d, vc_d = kc.to(device), vc.to(device)
+    if strided:
+        qkv_d = qkv.to(device)
+        k_d = qkv_d[:, 16 * D:(16 + Hkv) * D].view(T, Hkv, D)
+        v_d = qkv_d[:, (16 + Hkv) * D:].view(T, Hkv, D)
+    else:
+        k_d, v_d = k.to(device), v.to(device)
+    ops.kv_scatter(k_d, v_d, kc_d, vc_d, slots.to(device))
+    torch.cuda.synchronize()
+    kn, vn = kc.clone(), vc.clone()
+    oscat.kv_scatter(k.contiguous().view(torch.int16).numpy() if dtype != torch.float32 else k.contiguous().numpy(),
+                     v.contiguous().view(torch.int16).numpy() if dtype != torch.float32 else v.contiguous().numpy(),
+                     kn.view(torch.int16).numpy() if dtype != torch.float32 else kn.numpy(),
+                     vn.view(torch.int16).numpy() if dtype != torch.float32 else vn.numpy(),
+                     slots.numpy())
+    assert torch.equal(kc_d.cpu().view(torch.uint8), kn.view(torch.uint8))
+    assert torch.equal(vc_d.cpu().view(torch.uint8), vn.view(torch.uint8))
+
+
+def test_kv_scatter_config3_round_trip(device):
+    _say("kv_scatter config3 round trip")
+    step = workloads.mixed_step(seed=3)
+    b = step.batch
+    kc = torch.zeros_like(b.key_cache, device=device)
+    vc = torch.zeros_like(b.value_cache, device=device)
+    kc.fill_(7.0)
+    vc.fill_(-7.0)
+    slots = step.slot_mapping.to(device)
+    ops.kv_scatter(step.key.to(device), step.value.to(device), kc, vc, slots)
+    nb, bs = kc.shape[0], kc.shape[1]
+    flat_k = kc.view(nb * bs, *kc.shape[2:])
+    flat_v = vc.view(nb * bs, *vc.shape[2:])
+    assert torch.equal(flat_k[slots].cpu(), step.key)
+    assert torch.equal(flat_v[slots].cpu(), step.value)
+    touched = torch.zeros(nb * bs, dtype=torch.bool, device=device)
+    touched[slots] = True
+    assert bool((flat_k[~touched] == 7.0).all()) and bool((flat_v[~touched] == -7.0).all())
+
+
+# ---------------------------------------------------------------------------
+# paged attention
+# ---------------------------------------------------------------------------
+
+def _run_attention(batch: workloads.PagedBatch, device, use_cu: bool):
+    b = batch.to(device)
+    return ops.paged_attention(b.query, b.key_cache, b.value_cache, b.block_tables,
+                               b.context_lens, scale=b.scale,
+                               cu_seqlens=b.cu_seqlens if use_cu else None,
+                               num_decodes=b.num_decodes, max_query_len=b.max_query_len)
+
+
+def _oracle(batch: workloads.PagedBatch):
+    return oatt.mixed_attention(batch.query, batch.key_cache, batch.value_cache,
+                                batch.block_tables, batch.cu_seqlens, batch.context_lens,
+                                batch.scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("heads", [(16, 8, 128), (4, 2, 64), (8, 8, 128), (32, 4, 64), (16, 2, 128)])
+def test_decode_small_shapes(device, dtype, heads):
+    H, Hkv, D = heads
+    _say(f"decode small dtype={dtype} H={H} Hkv={Hkv} D={D}")
+    batch = workloads.paged_decode(seed=5, num_seqs=24, num_heads=H, num_kv_heads=Hkv,
+                                   head_dim=D, ctx_lo=1, ctx_hi=700, dtype=dtype,
+                                   scale_inputs=False, tail_fill=float("nan"),
+                                   ctx_head=[1, 15, 16, 17, 256, 257, 512, 513])
+    got = _run_attention(batch, device, use_cu=False)
+    _check_attention(got, _oracle(batch), f"decode {dtype} {heads}")
+
+
+@pytest.mark.parametrize("scaled", [True, False])
+def test_decode_config2(device, scaled):
+    _say(f"decode config2 scaled={scaled}")
+    batch = workloads.paged_decode(seed=0, scale_inputs=scaled)
+    got = _run_attention(batch, device, use_cu=False)
+    _check_attention(got, _oracle(batch), f"config2 scaled={scaled}")
+
+
+def test_decode_matches_reference_restatement(device):
+    """The literal _decode_fast restatement (gather over max_s, mask, einsum)."""
+    _say("decode vs literal _decode_fast restatement")
+    batch = workloads.paged_decode(seed=9, num_seqs=12, ctx_lo=1, ctx_hi=300, scale_inputs=False)
+    got = _run_attention(batch, device, use_cu=False)
+    ref = oatt.decode_attention(batch.query.float(), batch.key_cache.float(),
+                                batch.value_cache.float(), batch.block_tables,
+                                batch.context_lens, batch.scale)
+    _check_attention(got, ref, "literal restatement")
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_mixed_step_small(device, seed):
+    _say(f"mixed step small seed={seed}")
+    step = workloads.mixed_step(seed=seed, num_decodes=12, dec_lo=1, dec_hi=600, num_chunks=4,
+                                chunk_len=67, off_hi=300, num_cache_slots=16 * 400)
+    got = _run_attention(step.batch, device, use_cu=True)
+    _check_attention(got, _oracle(step.batch), f"mixed small seed={seed}")
+
+
+def test_prefill_only_offset_zero(device):
+    _say("prefill only, offset 0")
+    step = workloads.mixed_step(seed=4, num_decodes=0, num_chunks=3, chunk_len=100, off_lo=0,
+                                off_hi=0, num_cache_slots=16 * 64)
+    got = _run_attention(step.batch, device, use_cu=True)
+    _check_attention(got, _oracle(step.batch), "prefill offset 0")
+
+
+# ---------------------------------------------------------------------------
+# sampler
+# ---------------------------------------------------------------------------
+
+def test_sampler_config4(device):
+    _say("sampler config4")
+    sb = workloads.sampler_batch(seed=0)
+    got = ops.sample(sb.logits.to(device), sb.temperature.to(device), sb.uniform.to(device)).cpu()
+    x = sb.logits.float().numpy()
+    half = sb.logits.shape[0] // 2
+    # greedy rows: the planted maximum, bit-exact with argmax
+    assert torch.equal(got[:half], sb.planted[:half])
+    assert np.array_equal(got[:half].numpy(), osamp.greedy(x[:half]))
+    # temperature rows: bit-exact with the C restatement at the same uniforms
+    ref = osamp.sample(x[half:], sb.temperature[half:].numpy(), sb.uniform[half:].numpy())
+    assert np.array_equal(got[half:].numpy(), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("V", [1, 7, 511, 512, 513, 32000, 151936])
+def test_sampler_shapes(device, dtype, V):
+    _say(f"sampler dtype={dtype} V={V}")
+    g = torch.Generator().manual_seed(V)
+    B = 12
+    x = (torch.randn(B, V + 5, generator=g) * 3).to(dtype)[:, :V]   # row stride V + 5
+    if V > 4:
+        x[0, 1] = x[0, 3] = x[0].float().max() + 1   # tie: first index wins
+        x[1, : V // 2] = float("-inf")
+    temp = torch.tensor([0.0] * 4 + [0.6, 1.0, 1.7, 0.05, 1e-4, 2.0, 1.0, 1.0], dtype=torch.float32)
+    uni = torch.rand(B, generator=g)
+    uni[-2] = 0.0
+    uni[-1] = float(np.nextafter(np.float32(1), np.float32(0)))
+    xd = torch.empty(B, V + 5, dtype=dtype, device=device)[:, :V]
+    xd.copy_(x)
+    got = ops.sample(xd, temp.to(device), uni.to(device)).cpu().numpy()
+    ref = osamp.sample(x.float().numpy(), temp.numpy(), uni.numpy())
+    assert np.array_equal(got, ref)
+
+
+# ---------------------------------------------------------------------------
+# packing
+# ---------------------------------------------------------------------------
+
+KAT = json.loads((Path(__file__).parent / "golden" / "packing_kat.json").read_text())
+
+
+def _pack_on_gpu(device, descs, blocks, toks, bs, max_blocks, dev_toks=None):
+    T = int(np.asarray(descs)[:, 1].sum())
+    out = ops.pack_inputs(torch.as_tensor(descs, dtype=torch.int32).to(device),
+                          torch.as_tensor(blocks, dtype=torch.int32).to(device),
+                          torch.as_tensor(toks, dtype=torch.int64).to(device), T, bs, max_blocks,
+                          device_tokens=None if dev_toks is None else
+                          torch.as_tensor(dev_toks, dtype=torch.int64).to(device))
+    return {k: v.cpu().numpy() for k, v in out.items()}
+
+
+@pytest.mark.parametrize("case", KAT["cases"], ids=lambda c: c["name"])
+def test_pack_kat(device, case):
+    _say(f"pack kat {case['name']}")
+    recs = [opack.SeqRecord(s["prompt"], s["output"], s["num_computed"], s["blocks"])
+            for s in case["seqs"]]
+    descs, blocks, toks = opack.descriptors_from_records(recs)
+    got = _pack_on_gpu(device, descs, blocks, toks, KAT["block_size"], case["packed"]["max_blocks"])
+    for k in ("input_ids", "positions", "slot_mapping"):
+        assert got[k].tolist() == case["reference"][k], k
+    for k in ("cu_seqlens", "seq_start", "context_lens", "block_tables"):
+        assert got[k].tolist() == case["packed"][k], k
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_pack_random(device, seed):
+    _say(f"pack random seed={seed}")
+    rng = np.random.default_rng(seed)
+    B = int(rng.integers(1, 300))
+    bs = 16
+    descs, blocks, toks = [], [], []
+    dev_toks = rng.integers(0, 151936, 50)
+    for _ in range(B):
+        if rng.random() < 0.6:
+            n, q = int(rng.integers(0, 4000)), 1
+        else:
+            n, q = int(rng.integers(0, 3000)), int(rng.integers(1, 600))
+        nb = (n + q + bs - 1) // bs - int(rng.random() < 0.1)
+        tidx = int(rng.integers(0, 50)) if (q == 1 and rng.random() < 0.5) else -1
+        descs.append([n, q, max(nb, 0), len(blocks), len(toks), tidx])
+        blocks.extend(rng.integers(0, 12500, max(nb, 0)).tolist())
+        toks.extend(rng.integers(0, 151936, q).tolist())
+    descs = np.array(descs, dtype=np.int32)
+    blocks = np.array(blocks, dtype=np.int32)
+    toks = np.array(toks, dtype=np.int64)
+    mb = int(descs[:, 2].max()) if B else 0
+    got = _pack_on_gpu(device, descs, blocks, toks, bs, mb, dev_toks)
+    ref = opack.expand_descriptors(descs, blocks, toks, bs, mb, device_tokens=dev_toks)
+    for k in ref:
+        assert np.array_equal(got[k], ref[k]), k
+
+
+def test_pack_config3(device):
+    _say("pack config3")
+    step = workloads.mixed_step(seed=2)
+    mb = step.batch.block_tables.shape[1]
+    got = _pack_on_gpu(device, step.descs.numpy(), step.block_ids.numpy(),
+                       step.token_ids.numpy(), 16, mb)
+    assert np.array_equal(got["slot_mapping"], step.slot_mapping.numpy())
+    assert np.array_equal(got["positions"], step.positions.numpy())
+    assert np.array_equal(got["input_ids"], step.token_ids.numpy())
+    assert np.array_equal(got["cu_seqlens"], step.batch.cu_seqlens.numpy())
+    assert np.array_equal(got["context_lens"], step.batch.context_lens.numpy())
+    assert np.array_equal(got["block_tables"], step.batch.block_tables.numpy())
