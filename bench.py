@@ -73,6 +73,20 @@ def _median_cpu(fn, reps: int = 5) -> float:
     return statistics.median(ts)
 
 
+def _traffic(workload: str):
+    """Measured HBM bytes per call for `workload` from profiles/traffic.json
+    (rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by the copy calibration), or
+    None when no measurement is recorded."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text())
+    w = d.get(workload)
+    if not w or w.get("fetch_kib") is None or w.get("write_kib") is None:
+        return None
+    return int(w["fetch_kib"] * 1024 * d["fetch_scale"] + w["write_kib"] * 1024 * d["write_scale"])
+
+
 def decode_bytes(batch) -> int:
     """Algorithmic HBM bytes of one decode-attention pass: each live K/V row
     once, q and out once, the used block-table entries and context lengths."""
@@ -110,12 +124,13 @@ def bench_decode(args):
             "workload": "config2 paged decode attention: 256 seqs, ctx U[128,2048] (seed 0), "
                         "16 q / 8 kv heads, head_dim 128, block_size 16, bf16 in / fp32 accumulate",
             "num_seqs": 256, "sum_ctx": int(cpu_batch.context_lens.sum()),
-            "kernel": "lv_paged_attention (attn_rows_kernel + attn_reduce_kernel)",
-            "part_tokens": int(os.environ.get("LV_ATTN_PART_TOKENS", "256")),
+            "kernel": "lv_paged_attention (attn_decode_persistent_kernel + "
+                      "attn_persist_reduce_kernel)",
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": _traffic("decode"),
             "algorithmic_bytes": nbytes, "avg_launch_us": round(kern_ms * 1e3, 2),
         },
     }
@@ -173,7 +188,8 @@ def bench_sampler(args):
                                "rows 0-127 greedy, 128-255 T~U[0.5,1], supplied uniforms",
                    "kernel": "lv_sample (sampler_kernel)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": _traffic("sampler"),
                      "algorithmic_bytes": nbytes, "avg_launch_us": round(kern_ms * 1e3, 2)},
     }
     if not args.no_cpu_baseline:
@@ -226,12 +242,32 @@ def bench_mixed(args):
     }
 
 
+def bench_copy(args):
+    """Plain device copy of 1 GiB (torch copy_): the calibration kernel for
+    the HBM byte counters and the achievable-bandwidth reference."""
+    import torch
+    dev = torch.device("cuda:0")
+    n = 1 << 29  # bf16 elements = 1 GiB
+    src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    total_ms, per = _time_gpu(lambda: dst.copy_(src), args.steps, args.warmup)
+    kern_ms = statistics.mean(per)
+    nbytes = 2 * n * 2
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    return {"value": round(achieved, 1), "unit": "GB/s", "ms_per_step": round(total_ms / args.steps, 4),
+            "config": {"workload": "calibration: torch copy_ of 1 GiB bf16 (1 GiB read + 1 GiB write)",
+                       "bytes_read": n * 2, "bytes_written": n * 2},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "algorithmic_bytes": nbytes, "avg_launch_us": round(kern_ms * 1e3, 2)}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "sampler", "mixed"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "sampler", "mixed", "copy"], default="decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -242,7 +278,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
-    fn = {"decode": bench_decode, "sampler": bench_sampler, "mixed": bench_mixed}[args.workload]
+    fn = {"decode": bench_decode, "sampler": bench_sampler, "mixed": bench_mixed,
+          "copy": bench_copy}[args.workload]
     res = fn(args)
     line = {
         "metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1,

@@ -156,7 +156,8 @@ int lv_kv_scatter(const void* key_dev, int64_t key_stride_t,
  * outside [0, num_cache_blocks) reads block 0 instead of faulting); context
  * lengths are clamped to max_blocks * block_size.
  * workspace: at least lv_paged_attention_workspace_size(...) bytes, 256-B
- * aligned; contents need not be initialised.
+ * aligned; contents need not be initialised.  Calls that overlap on one
+ * workspace race (use one workspace per stream).
  * Supported: head_dim 64 or 128, block_size 16, num_heads / num_kv_heads in
  * {1, 2, 4, 8}; anything else returns LV_ERR_UNSUPPORTED.
  */

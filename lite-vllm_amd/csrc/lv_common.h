@@ -100,6 +100,13 @@ template <> struct elem<f16> {
 __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
+// Streaming 16-byte load (non-temporal hint: data read once, not cached for
+// reuse).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load16_nt(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ void store16(void* p, const uint4& v) {
   *reinterpret_cast<uint4*>(p) = v;
 }

@@ -20,6 +20,8 @@
 // workspace and are merged by attn_reduce_kernel.
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "lv_common.h"
 
 namespace lv {
@@ -59,85 +61,57 @@ __device__ __forceinline__ void resolve_row(int row, const int32_t* __restrict__
   limit = min(limit, max_tokens);
 }
 
-template <typename T, int D, int G, int BS>
-__global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(
-    const T* __restrict__ q, int64_t q_stride,
-    const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
-    const int32_t* __restrict__ block_tables, int max_blocks,
-    const int32_t* __restrict__ cu, int num_seqs, const int32_t* __restrict__ ctx,
-    int row_begin, int part_tokens, int max_parts, float scale_log2,
-    T* __restrict__ out, int64_t out_stride,
-    float* __restrict__ ws_acc, float* __restrict__ ws_ml) {
+// Online-softmax state of one wavefront for one kv head and the G query
+// heads that read it.  Lane = (token-in-load tg, dim chunk dc); every value
+// below is per lane.  Scores are kept in log2 units (q pre-scaled by
+// scale * log2(e)).
+template <typename T, int D, int G, int BS, bool NT>
+struct HeadState {
   using C = RowCfg<T, D, BS>;
-  constexpr int VEC = C::VEC, RL = C::ROW_LANES, TPL = C::TPL, LOADS = C::LOADS;
-  __shared__ float s_acc[kAttnWaves][G][D];
-  __shared__ float s_m[kAttnWaves][G];
-  __shared__ float s_l[kAttnWaves][G];
-
-  const int row = row_begin + (int)blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int part = blockIdx.z;
-  int seq, limit;
-  resolve_row(row, cu, num_seqs, ctx, max_blocks * BS, seq, limit);
-  const int start = part * part_tokens;
-  if (start >= limit) return;
-  const int end = min(limit, start + part_tokens);
-  const int nparts = (limit + part_tokens - 1) / part_tokens;
-
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int tg = lane / RL;
-  const int dc = lane % RL;
-
+  static constexpr int VEC = C::VEC, RL = C::ROW_LANES, TPL = C::TPL, LOADS = C::LOADS;
   float qv[G][VEC];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const T* qp = q + (int64_t)row * q_stride + (int64_t)(kvh * G + g) * D + dc * VEC;
-    elem<T>::unpack(load16(qp), qv[g]);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) qv[g][j] *= scale_log2;
-  }
-
   float m[G], l[G], acc[G][VEC];
+  int tg, dc;
+
+  __device__ __forceinline__ void init(const T* __restrict__ qhead, float scale_log2, int lane) {
+    tg = lane / RL;
+    dc = lane % RL;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kNegBig;
-    l[g] = 0.0f;
+    for (int g = 0; g < G; ++g) {
+      elem<T>::unpack(load16(qhead + (int64_t)g * D + dc * VEC), qv[g]);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) acc[g][j] = 0.0f;
+      for (int j = 0; j < VEC; ++j) qv[g][j] *= scale_log2;
+      m[g] = kNegBig;
+      l[g] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[g][j] = 0.0f;
+    }
   }
 
-  const int64_t tok_stride = (int64_t)num_kv_heads * D;
-  const int64_t blk_stride = (int64_t)BS * tok_stride;
-  const int64_t lane_off = (int64_t)kvh * D + dc * VEC + tg * tok_stride;
-  const int32_t* __restrict__ bt = block_tables + (int64_t)seq * max_blocks;
-  const int b_begin = start / BS;
-  const int b_end = (end + BS - 1) / BS;
-
-  auto load_block = [&](int b, uint4* kk, uint4* vv) {
-    int64_t phys = bt[b];
-    if (phys < 0 || phys >= num_cache_blocks) phys = 0;
-    const T* kp = kc + phys * blk_stride + lane_off;
-    const T* vp = vc + phys * blk_stride + lane_off;
+  // K and V rows of this lane's tokens in physical block `phys`.
+  __device__ __forceinline__ void load(const T* __restrict__ kbase, const T* __restrict__ vbase,
+                                       int64_t phys, int64_t blk_stride, int64_t tok_stride,
+                                       uint4* kk, uint4* vv) const {
+    const T* kp = kbase + phys * blk_stride;
+    const T* vp = vbase + phys * blk_stride;
 #pragma unroll
-    for (int r = 0; r < LOADS; ++r) kk[r] = load16(kp + (int64_t)r * TPL * tok_stride);
+    for (int r = 0; r < LOADS; ++r)
+      kk[r] = NT ? load16_nt(kp + (int64_t)r * TPL * tok_stride)
+                 : load16(kp + (int64_t)r * TPL * tok_stride);
 #pragma unroll
-    for (int r = 0; r < LOADS; ++r) vv[r] = load16(vp + (int64_t)r * TPL * tok_stride);
-  };
+    for (int r = 0; r < LOADS; ++r)
+      vv[r] = NT ? load16_nt(vp + (int64_t)r * TPL * tok_stride)
+                 : load16(vp + (int64_t)r * TPL * tok_stride);
+  }
 
-  uint4 kr[LOADS], vr[LOADS];
-  int blk = b_begin + wave;
-  if (blk < b_end) load_block(blk, kr, vr);
-  for (; blk < b_end; blk += kAttnWaves) {
-    uint4 kn[LOADS], vn[LOADS];
-    const int nb = blk + kAttnWaves;
-    if (nb < b_end) load_block(nb, kn, vn);
-
+  // Fold logical block `blk` (positions blk*BS ..) into the state; positions
+  // >= end are masked.
+  __device__ __forceinline__ void process(const uint4* kk, const uint4* vv, int blk, int end) {
     float s[G][LOADS];
 #pragma unroll
     for (int r = 0; r < LOADS; ++r) {
       float kf[VEC];
-      elem<T>::unpack(kr[r], kf);
+      elem<T>::unpack(kk[r], kf);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float d = 0.0f;
@@ -171,7 +145,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(
 #pragma unroll
     for (int r = 0; r < LOADS; ++r) {
       float vf[VEC];
-      elem<T>::unpack(vr[r], vf);
+      elem<T>::unpack(vv[r], vf);
       if (tail && pos0 + r * TPL >= end) {
         // Slots past the context may hold anything (even NaN); 0 * NaN
         // would poison the accumulator, so drop them explicitly.
@@ -183,36 +157,113 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(
 #pragma unroll
         for (int j = 0; j < VEC; ++j) acc[g][j] = fmaf(s[g][r], vf[j], acc[g][j]);
     }
-    if (nb < b_end) {
-#pragma unroll
-      for (int r = 0; r < LOADS; ++r) { kr[r] = kn[r]; vr[r] = vn[r]; }
+  }
+
+  // Stream blocks first, first+stride, ... (n of them) through process().
+  // Block ids are fetched 64 at a time with one vector load and handed out
+  // with readlane, so no K/V load waits on a block-table read.  Two register
+  // buffers alternate: block i+1 is in flight while block i is computed.
+  // Every prefetch and every process() is unconditional (the index of a
+  // block past the end is clamped to the last one, whose reload hits in
+  // cache, and its positions are all masked), so no load sits under a branch
+  // where the compiler would sink it next to its use or drain all loads at
+  // the join.
+  __device__ __forceinline__ void stream(const int32_t* __restrict__ bt, int first, int stride,
+                                         int n, int end, const T* __restrict__ kbase,
+                                         const T* __restrict__ vbase, int64_t blk_stride,
+                                         int64_t tok_stride, int64_t num_cache_blocks, int lane) {
+    uint4 k0[LOADS], v0[LOADS], k1[LOADS], v1[LOADS];
+    for (int base = 0; base < n; base += 64) {
+      const int cnt = min(64, n - base);
+      int id = 0;
+      if (lane < cnt) id = bt[first + stride * (base + lane)];
+      if (id < 0 || id >= num_cache_blocks) id = 0;
+      auto phys = [&](int i) { return __builtin_amdgcn_readlane(id, min(i, cnt - 1)); };
+      load(kbase, vbase, phys(0), blk_stride, tok_stride, k0, v0);
+      for (int i = 0; i < cnt; i += 2) {
+        load(kbase, vbase, phys(i + 1), blk_stride, tok_stride, k1, v1);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the math
+        process(k0, v0, first + stride * (base + i), end);
+        load(kbase, vbase, phys(i + 2), blk_stride, tok_stride, k0, v0);
+        __builtin_amdgcn_sched_barrier(0);
+        // Unconditional, so the k1/v1 loads have a use on every path and are
+        // not sunk next to it; past the last block every position is masked
+        // (end = -1), which leaves the state unchanged.
+        process(k1, v1, first + stride * (base + i + 1), i + 1 < cnt ? end : -1);
+      }
     }
   }
 
-  // Merge the TPL token groups of this wavefront.
+  // Merge the TPL token groups of the wavefront (lanes RL apart).
+  __device__ __forceinline__ void merge_token_groups() {
 #pragma unroll
-  for (int ofs = RL; ofs < 64; ofs <<= 1) {
+    for (int ofs = RL; ofs < 64; ofs <<= 1) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mo = __shfl_xor(m[g], ofs);
-      const float lo = __shfl_xor(l[g], ofs);
-      const float mn = fmaxf(m[g], mo);
-      const float fa = fast_exp2(m[g] - mn), fb = fast_exp2(mo - mn);
-      l[g] = l[g] * fa + lo * fb;
+      for (int g = 0; g < G; ++g) {
+        const float mo = __shfl_xor(m[g], ofs);
+        const float lo = __shfl_xor(l[g], ofs);
+        const float mn = fmaxf(m[g], mo);
+        const float fa = fast_exp2(m[g] - mn), fb = fast_exp2(mo - mn);
+        l[g] = l[g] * fa + lo * fb;
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const float ao = __shfl_xor(acc[g][j], ofs);
-        acc[g][j] = acc[g][j] * fa + ao * fb;
+        for (int j = 0; j < VEC; ++j) {
+          const float ao = __shfl_xor(acc[g][j], ofs);
+          acc[g][j] = acc[g][j] * fa + ao * fb;
+        }
+        m[g] = mn;
       }
-      m[g] = mn;
     }
   }
-  if (tg == 0) {
+};
+
+// One workgroup (4 wavefronts) per (query row, kv head, context partition);
+// wavefront w takes blocks w, w+4, ... of the partition and the four states
+// are merged through LDS.
+template <typename T, int D, int G, int BS, bool NT>
+__global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(
+    const T* __restrict__ q, int64_t q_stride,
+    const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
+    const int32_t* __restrict__ block_tables, int max_blocks,
+    const int32_t* __restrict__ cu, int num_seqs, const int32_t* __restrict__ ctx,
+    int row_begin, int part_tokens, int max_parts, float scale_log2,
+    T* __restrict__ out, int64_t out_stride,
+    float* __restrict__ ws_acc, float* __restrict__ ws_ml) {
+  using S = HeadState<T, D, G, BS, NT>;
+  constexpr int VEC = S::VEC;
+  __shared__ float s_acc[kAttnWaves][G][D];
+  __shared__ float s_m[kAttnWaves][G];
+  __shared__ float s_l[kAttnWaves][G];
+
+  const int row = row_begin + (int)blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int part = blockIdx.z;
+  int seq, limit;
+  resolve_row(row, cu, num_seqs, ctx, max_blocks * BS, seq, limit);
+  const int start = part * part_tokens;
+  if (start >= limit) return;
+  const int end = min(limit, start + part_tokens);
+  const int nparts = (limit + part_tokens - 1) / part_tokens;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+
+  S st;
+  st.init(q + (int64_t)row * q_stride + (int64_t)kvh * G * D, scale_log2, lane);
+  const int64_t tok_stride = (int64_t)num_kv_heads * D;
+  const int64_t lane_off = (int64_t)kvh * D + st.dc * VEC + st.tg * tok_stride;
+  const int b_begin = start / BS;
+  const int b_end = (end + BS - 1) / BS;
+  const int first = b_begin + wave;
+  const int n = first < b_end ? (b_end - first + kAttnWaves - 1) / kAttnWaves : 0;
+  st.stream(block_tables + (int64_t)seq * max_blocks, first, kAttnWaves, n, end, kc + lane_off,
+            vc + lane_off, (int64_t)BS * tok_stride, tok_stride, num_cache_blocks, lane);
+  st.merge_token_groups();
+
+  if (st.tg == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) s_acc[wave][g][dc * VEC + j] = acc[g][j];
-      if (dc == 0) { s_m[wave][g] = m[g]; s_l[wave][g] = l[g]; }
+      for (int j = 0; j < VEC; ++j) s_acc[wave][g][st.dc * VEC + j] = st.acc[g][j];
+      if (st.dc == 0) { s_m[wave][g] = st.m[g]; s_l[wave][g] = st.l[g]; }
     }
   }
   __syncthreads();
@@ -242,8 +293,231 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent decode kernel.
+//
+// The blocks of all decode sequences form one flattened list (sequence-major:
+// sequence s owns entries off[s] .. off[s+1]-1, off = exclusive scan of
+// ceil(ctx / bs)).  A fixed grid of workgroups (about two per CU) splits the
+// list into equal contiguous ranges, so every workgroup streams the same
+// number of blocks however ragged the contexts are.  Wavefront w of a
+// workgroup owns kv head w; all wavefronts walk the same blocks, so the K/V
+// rows of all heads of a block -- one contiguous run in HBM -- are read
+// together.  A wavefront streams its whole range without draining: when the
+// next block belongs to another sequence it finishes the current one and
+// starts the next.  A sequence lying entirely inside one range is written
+// straight to `out`; only the first and last piece of a range can be partial
+// (slot 0 / slot 1 of that workgroup), and attn_persist_reduce_kernel merges
+// the pieces of sequences that span several ranges (the kernel boundary
+// orders the partial writes before their reads without any device-scope
+// fence inside the streaming kernel).
+// ---------------------------------------------------------------------------
+constexpr int kPersistMaxWaves = 8;  // kv heads per workgroup (one wavefront each)
+constexpr int kPersistMaxSeqs = 15000;  // (B+1) ints of LDS stay under 60 KB
+
+// Exclusive scan of ceil(min(ctx, max_tokens) / bs) into s_off[0..n] by one
+// workgroup (integer, order-independent).
+template <int BS>
+__device__ void scan_block_counts(const int32_t* __restrict__ ctx, int n, int max_tokens,
+                                  int32_t* s_off, int32_t* s_part) {
+  const int t = threadIdx.x, nt = blockDim.x;
+  const int per = (n + nt - 1) / nt;
+  const int lo = min(n, t * per), hi = min(n, lo + per);
+  int32_t sum = 0;
+  for (int i = lo; i < hi; ++i) sum += (min(max(ctx[i], 0), max_tokens) + BS - 1) / BS;
+  s_part[t] = sum;
+  __syncthreads();
+  for (int d = 1; d < nt; d <<= 1) {
+    const int32_t v = (t >= d) ? s_part[t - d] : 0;
+    __syncthreads();
+    s_part[t] += v;
+    __syncthreads();
+  }
+  int32_t run = (t == 0) ? 0 : s_part[t - 1];
+  for (int i = lo; i < hi; ++i) {
+    s_off[i] = run;
+    run += (min(max(ctx[i], 0), max_tokens) + BS - 1) / BS;
+  }
+  if (t == nt - 1) s_off[n] = s_part[nt - 1];
+  __syncthreads();
+}
+
+template <typename T, int D, int G, int BS, bool NT, int NBUF>
+__global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_kernel(
+    const T* __restrict__ q, int64_t q_stride,
+    const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
+    const int32_t* __restrict__ block_tables, int max_blocks, const int32_t* __restrict__ ctx,
+    int num_seqs, float scale_log2, T* __restrict__ out, int64_t out_stride,
+    int32_t* __restrict__ ws_off, float* __restrict__ ws_acc, float* __restrict__ ws_ml) {
+  using S = HeadState<T, D, G, BS, NT>;
+  constexpr int VEC = S::VEC;
+  extern __shared__ int32_t s_off[];               // num_seqs + 1
+  __shared__ int32_t s_part[kPersistMaxWaves * 64];
+  const int max_tokens = max_blocks * BS;
+  scan_block_counts<BS>(ctx, num_seqs, max_tokens, s_off, s_part);
+  const int total = s_off[num_seqs];
+  const int H = num_kv_heads * G;
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i <= num_seqs; i += blockDim.x) ws_off[i] = s_off[i];
+  if (total == 0) return;
+  const int per = (total + gridDim.x - 1) / gridDim.x;
+  const int r0 = blockIdx.x * per;
+  const int r1 = min(total, r0 + per);
+  if (r0 >= r1) return;
+
+  const int lane = threadIdx.x & 63;
+  const int kvh = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (kvh >= num_kv_heads) return;
+  const int64_t tok_stride = (int64_t)num_kv_heads * D;
+  const int64_t blk_stride = (int64_t)BS * tok_stride;
+
+  S st;
+  st.tg = lane / S::RL;
+  st.dc = lane % S::RL;
+  const int64_t lane_off = (int64_t)kvh * D + st.dc * VEC + st.tg * tok_stride;
+  const T* kbase = kc + lane_off;
+  const T* vbase = vc + lane_off;
+
+  int cur = -1;     // sequence whose state st holds (uniform)
+  int cur_end = 0;  // its context length
+
+  // Finish sequence sq: a piece covering the whole sequence goes straight to
+  // `out`, any other piece to this workgroup's slot 0 (first piece) or 1.
+  auto finish = [&](int sq) {
+    st.merge_token_groups();
+    const int a = s_off[sq], b = s_off[sq + 1];
+    const bool whole = a >= r0 && b <= r1;
+    if (st.tg != 0) return;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int hq = kvh * G + g;
+      const float inv = st.l[g] > 0.0f ? 1.0f / st.l[g] : 0.0f;
+      if (whole) {
+        T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + st.dc * VEC;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, st.acc[g][j] * inv);
+      } else {
+        const int slot = (a <= r0) ? 0 : 1;
+        const int64_t base = ((int64_t)blockIdx.x * 2 + slot) * H + hq;
+        float* wp = ws_acc + base * D + st.dc * VEC;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) wp[j] = st.acc[g][j] * inv;
+        if (st.dc == 0) { ws_ml[base * 2] = st.m[g]; ws_ml[base * 2 + 1] = st.l[g]; }
+      }
+    }
+  };
+
+  static_assert(NBUF == 2 || NBUF == 4, "NBUF");
+  uint4 k0[S::LOADS], v0[S::LOADS], k1[S::LOADS], v1[S::LOADS];
+  uint4 k2[NBUF == 4 ? S::LOADS : 1], v2[NBUF == 4 ? S::LOADS : 1];
+  uint4 k3[NBUF == 4 ? S::LOADS : 1], v3[NBUF == 4 ? S::LOADS : 1];
+  for (int base = r0; base < r1; base += 64) {
+    const int cnt = min(64, r1 - base);
+    // Lane i resolves flattened entry base + i: its sequence, logical block
+    // and physical block id.
+    int lseq = 0, lblk = 0, id = 0;
+    if (lane < cnt) {
+      const int j = base + lane;
+      int lo = 0, hi = num_seqs - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_off[mid] <= j) lo = mid; else hi = mid - 1;
+      }
+      lseq = lo;
+      lblk = j - s_off[lo];
+      id = block_tables[(int64_t)lo * max_blocks + lblk];
+    }
+    if (id < 0 || id >= num_cache_blocks) id = 0;
+    auto phys = [&](int i) { return __builtin_amdgcn_readlane(id, min(i, cnt - 1)); };
+    // Start (or continue) the sequence of entry i, then fold its block in;
+    // i >= cnt is a fully masked no-op so process() always runs.
+    auto visit = [&](const uint4* kk, const uint4* vv, int i) {
+      const bool real = i < cnt;
+      const int sq = __builtin_amdgcn_readlane(lseq, min(i, cnt - 1));
+      const int lb = __builtin_amdgcn_readlane(lblk, min(i, cnt - 1));
+      if (real && sq != cur) {
+        if (cur >= 0) finish(cur);
+        cur = sq;
+        cur_end = min(max(ctx[sq], 0), max_tokens);
+        st.init(q + (int64_t)sq * q_stride + (int64_t)kvh * G * D, scale_log2, lane);
+      }
+      st.process(kk, vv, lb, real ? cur_end : -1);
+    };
+    // NBUF register buffers rotate: NBUF - 1 blocks are in flight while one
+    // is folded in.  Loads past the group end reload its last block (cache
+    // hit) and their visits are masked no-ops.
+    if constexpr (NBUF == 2) {
+      st.load(kbase, vbase, phys(0), blk_stride, tok_stride, k0, v0);
+      for (int i = 0; i < cnt; i += 2) {
+        st.load(kbase, vbase, phys(i + 1), blk_stride, tok_stride, k1, v1);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k0, v0, i);
+        st.load(kbase, vbase, phys(i + 2), blk_stride, tok_stride, k0, v0);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k1, v1, i + 1);
+      }
+    } else {
+      st.load(kbase, vbase, phys(0), blk_stride, tok_stride, k0, v0);
+      st.load(kbase, vbase, phys(1), blk_stride, tok_stride, k1, v1);
+      st.load(kbase, vbase, phys(2), blk_stride, tok_stride, k2, v2);
+      for (int i = 0; i < cnt; i += 4) {
+        st.load(kbase, vbase, phys(i + 3), blk_stride, tok_stride, k3, v3);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k0, v0, i);
+        st.load(kbase, vbase, phys(i + 4), blk_stride, tok_stride, k0, v0);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k1, v1, i + 1);
+        st.load(kbase, vbase, phys(i + 5), blk_stride, tok_stride, k1, v1);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k2, v2, i + 2);
+        st.load(kbase, vbase, phys(i + 6), blk_stride, tok_stride, k2, v2);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k3, v3, i + 3);
+      }
+    }
+  }
+  if (cur >= 0) finish(cur);
+}
+
+// Merge the pieces of every sequence that spans several workgroup ranges
+// (same flattened split as the persistent kernel); write zeros for a
+// sequence with no tokens.
+template <typename T, int D>
+__global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
+    const int32_t* __restrict__ ws_off, int num_seqs, int num_wgs, int num_heads,
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
+    T* __restrict__ out, int64_t out_stride) {
+  const int sq = blockIdx.x;
+  const int hq = blockIdx.y;
+  const int d = threadIdx.x;
+  const int total = ws_off[num_seqs];
+  const int a = ws_off[sq], b = ws_off[sq + 1];
+  T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + d;
+  if (a == b) {
+    elem<T>::store(op, 0.0f);
+    return;
+  }
+  const int per = (total + num_wgs - 1) / num_wgs;
+  const int g0 = a / per, g1 = (b - 1) / per;
+  if (g0 == g1) return;
+  float M = kNegBig;
+  for (int g = g0; g <= g1; ++g) {
+    const int slot = (a <= g * per) ? 0 : 1;
+    M = fmaxf(M, ws_ml[(((int64_t)g * 2 + slot) * num_heads + hq) * 2]);
+  }
+  float L = 0.0f, O = 0.0f;
+  for (int g = g0; g <= g1; ++g) {
+    const int slot = (a <= g * per) ? 0 : 1;
+    const int64_t base = ((int64_t)g * 2 + slot) * num_heads + hq;
+    const float f = ws_ml[base * 2 + 1] * fast_exp2(ws_ml[base * 2] - M);
+    L += f;
+    O = fmaf(ws_acc[base * D + d], f, O);
+  }
+  elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
+}
+
 // Merge the partitions of one (row, query head); rows with a single
-// partition were finished by attn_rows_kernel.
+// partition were finished by the attention kernel.
 template <typename T, int D, int BS>
 __global__ __launch_bounds__(D) void attn_reduce_kernel(
     const int32_t* __restrict__ cu, int num_seqs, const int32_t* __restrict__ ctx, int max_blocks,
@@ -273,36 +547,71 @@ __global__ __launch_bounds__(D) void attn_reduce_kernel(
 // Host side.
 // ---------------------------------------------------------------------------
 
-// Context partition length (tokens) for split-K decode: a multiple of
-// 4 * block_size so each wavefront gets whole blocks.
-static int decode_part_tokens(int block_size) {
-  int pt = 256;
-  if (const char* e = getenv("LV_ATTN_PART_TOKENS")) {
-    const int v = atoi(e);
-    if (v > 0) pt = v;
-  }
-  const int unit = kAttnWaves * block_size;
-  pt = ((pt + unit - 1) / unit) * unit;
-  return pt;
+// Decode kernel choice.  Default: the persistent kernel with non-temporal
+// K/V loads.  Tuning knobs (environment): LV_ATTN_DECODE_KERNEL=rows selects
+// the workgroup-per-(row, kv head, partition) kernel, LV_ATTN_PART_TOKENS its
+// partition length, LV_ATTN_NT=0 plain loads, LV_ATTN_PERSIST_WGS the
+// persistent grid size.
+static bool env_is(const char* name, char c) {
+  const char* e = getenv(name);
+  return e != nullptr && e[0] == c;
+}
+
+static int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  if (e == nullptr) return dflt;
+  const int v = atoi(e);
+  return v > 0 ? v : dflt;
+}
+
+// CU count of the current device (queried once per device).
+static int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct AttnPlan {
-  int part_tokens;
-  int max_parts;
-  size_t acc_bytes, ml_bytes;
+  bool persistent;
+  bool nt;
+  int nbuf;         // persistent kernel: blocks in flight per wavefront + 1
+  int part_tokens;  // rows kernel
+  int max_parts;    // rows kernel
+  int num_wgs;      // persistent kernel
+  size_t off_bytes, ml_bytes, acc_bytes;  // off_bytes: flattened block offsets
+  size_t bytes() const { return off_bytes + ml_bytes + acc_bytes; }
 };
 
-static AttnPlan plan_decode(int num_decodes, int num_heads, int head_dim, int block_size,
-                            int max_blocks) {
-  AttnPlan p;
+static AttnPlan plan_decode(int num_decodes, int num_heads, int num_kv_heads, int head_dim,
+                            int block_size, int max_blocks) {
+  AttnPlan p{};
+  p.nt = !env_is("LV_ATTN_NT", '0');
+  p.persistent = !env_is("LV_ATTN_DECODE_KERNEL", 'r') && num_kv_heads <= kPersistMaxWaves &&
+                 num_decodes <= kPersistMaxSeqs;
+  if (p.persistent) {
+    // One workgroup of num_kv_heads wavefronts per CU; each wavefront keeps
+    // NBUF - 1 blocks (8 KiB each at the Qwen3 shape) in flight.
+    p.nbuf = env_int("LV_ATTN_NBUF", 2) == 4 ? 4 : 2;
+    p.num_wgs = env_int("LV_ATTN_PERSIST_WGS", device_cu_count() * (num_kv_heads == 1 ? 4 : 1));
+    p.off_bytes = align256(sizeof(int32_t) * (size_t)(num_decodes + 1));
+    p.ml_bytes = align256(sizeof(float) * 2 * (size_t)p.num_wgs * 2 * num_heads);
+    p.acc_bytes = align256(sizeof(float) * (size_t)p.num_wgs * 2 * num_heads * head_dim);
+    return p;
+  }
+  const int unit = kAttnWaves * block_size;
+  p.part_tokens = ((env_int("LV_ATTN_PART_TOKENS", 256) + unit - 1) / unit) * unit;
   const int max_tokens = max_blocks * block_size;
-  p.part_tokens = decode_part_tokens(block_size);
   p.max_parts = max_tokens > 0 ? (max_tokens + p.part_tokens - 1) / p.part_tokens : 1;
   if (p.max_parts <= 1) {
     p.max_parts = 1;
-    p.acc_bytes = p.ml_bytes = 0;
   } else {
     const size_t n = (size_t)num_decodes * num_heads * p.max_parts;
     p.acc_bytes = align256(n * head_dim * sizeof(float));
@@ -311,7 +620,7 @@ static AttnPlan plan_decode(int num_decodes, int num_heads, int head_dim, int bl
   return p;
 }
 
-template <typename T, int D, int G, int BS>
+template <typename T, int D, int G, int BS, bool NT>
 static void launch_rows(const void* q, int64_t q_stride, const void* kc, const void* vc,
                         int num_kv_heads, int64_t num_cache_blocks, const int32_t* bt,
                         int max_blocks, const int32_t* cu, int num_seqs, const int32_t* ctx,
@@ -319,7 +628,7 @@ static void launch_rows(const void* q, int64_t q_stride, const void* kc, const v
                         float scale_log2, void* out, int64_t out_stride, float* ws_acc,
                         float* ws_ml, hipStream_t st) {
   const dim3 grid(n_rows, num_kv_heads, max_parts);
-  hipLaunchKernelGGL((attn_rows_kernel<T, D, G, BS>), grid, dim3(kAttnThreads), 0, st,
+  hipLaunchKernelGGL((attn_rows_kernel<T, D, G, BS, NT>), grid, dim3(kAttnThreads), 0, st,
                      (const T*)q, q_stride, (const T*)kc, (const T*)vc, num_kv_heads,
                      num_cache_blocks, bt, max_blocks, cu, num_seqs, ctx, row_begin, part_tokens,
                      max_parts, scale_log2, (T*)out, out_stride, ws_acc, ws_ml);
@@ -331,49 +640,93 @@ static void launch_rows(const void* q, int64_t q_stride, const void* kc, const v
   }
 }
 
+template <typename T, int D, int G, int BS, bool NT, int NBUF>
+static void launch_persistent(const void* q, int64_t q_stride, const void* kc, const void* vc,
+                              int num_kv_heads, int64_t num_cache_blocks, const int32_t* bt,
+                              int max_blocks, const int32_t* ctx, int num_seqs, float scale_log2,
+                              void* out, int64_t out_stride, const AttnPlan& p, char* ws,
+                              hipStream_t st) {
+  int32_t* ws_off = (int32_t*)ws;
+  float* ws_ml = (float*)(ws + p.off_bytes);
+  float* ws_acc = (float*)(ws + p.off_bytes + p.ml_bytes);
+  const size_t lds = sizeof(int32_t) * (size_t)(num_seqs + 1);
+  hipLaunchKernelGGL((attn_decode_persistent_kernel<T, D, G, BS, NT, NBUF>), dim3(p.num_wgs),
+                     dim3(64 * num_kv_heads), lds, st, (const T*)q, q_stride, (const T*)kc,
+                     (const T*)vc, num_kv_heads, num_cache_blocks, bt, max_blocks, ctx, num_seqs,
+                     scale_log2, (T*)out, out_stride, ws_off, ws_acc, ws_ml);
+  hipLaunchKernelGGL((attn_persist_reduce_kernel<T, D>), dim3(num_seqs, num_kv_heads * G),
+                     dim3(D), 0, st, (const int32_t*)ws_off, num_seqs, p.num_wgs,
+                     num_kv_heads * G, (const float*)ws_acc, (const float*)ws_ml, (T*)out,
+                     out_stride);
+}
+
+// Everything one launch needs besides the dtype / shape template arguments.
+struct LaunchArgs {
+  const void* q; int64_t q_stride; const void* kc; const void* vc; int num_kv_heads;
+  int64_t num_cache_blocks; const int32_t* bt; int max_blocks; const int32_t* cu; int num_seqs;
+  const int32_t* ctx; int row_begin; int n_rows; float scale_log2; void* out; int64_t out_stride;
+  hipStream_t st;
+};
+
+template <typename T, int D, int G, int BS>
+static void launch(const LaunchArgs& a, const AttnPlan& p, char* ws) {
+  float* ws_ml = ws ? (float*)(ws + p.off_bytes) : nullptr;
+  float* ws_acc = ws ? (float*)(ws + p.off_bytes + p.ml_bytes) : nullptr;
+  if (p.persistent) {
+#define LV_PERSIST(NT_, NB_)                                                                    \
+  launch_persistent<T, D, G, BS, NT_, NB_>(a.q, a.q_stride, a.kc, a.vc, a.num_kv_heads,        \
+                                           a.num_cache_blocks, a.bt, a.max_blocks, a.ctx,       \
+                                           a.n_rows, a.scale_log2, a.out, a.out_stride, p, ws,  \
+                                           a.st)
+    if (p.nt && p.nbuf == 4) LV_PERSIST(true, 4);
+    else if (p.nt) LV_PERSIST(true, 2);
+    else if (p.nbuf == 4) LV_PERSIST(false, 4);
+    else LV_PERSIST(false, 2);
+#undef LV_PERSIST
+  } else if (p.nt) {
+    launch_rows<T, D, G, BS, true>(a.q, a.q_stride, a.kc, a.vc, a.num_kv_heads,
+                                   a.num_cache_blocks, a.bt, a.max_blocks, a.cu, a.num_seqs, a.ctx,
+                                   a.row_begin, a.n_rows, p.part_tokens, p.max_parts, a.scale_log2,
+                                   a.out, a.out_stride, ws_acc, ws_ml, a.st);
+  } else {
+    launch_rows<T, D, G, BS, false>(a.q, a.q_stride, a.kc, a.vc, a.num_kv_heads,
+                                    a.num_cache_blocks, a.bt, a.max_blocks, a.cu, a.num_seqs,
+                                    a.ctx, a.row_begin, a.n_rows, p.part_tokens, p.max_parts,
+                                    a.scale_log2, a.out, a.out_stride, ws_acc, ws_ml, a.st);
+  }
+}
 template <typename T, int D, int BS>
-static int dispatch_g(int G, const void* q, int64_t q_stride, const void* kc, const void* vc,
-                      int num_kv_heads, int64_t num_cache_blocks, const int32_t* bt, int max_blocks,
-                      const int32_t* cu, int num_seqs, const int32_t* ctx, int row_begin,
-                      int n_rows, int part_tokens, int max_parts, float scale_log2, void* out,
-                      int64_t out_stride, float* ws_acc, float* ws_ml, hipStream_t st) {
-#define LV_ROWS(GG)                                                                              \
-  launch_rows<T, D, GG, BS>(q, q_stride, kc, vc, num_kv_heads, num_cache_blocks, bt, max_blocks, \
-                            cu, num_seqs, ctx, row_begin, n_rows, part_tokens, max_parts,         \
-                            scale_log2, out, out_stride, ws_acc, ws_ml, st)
+static int dispatch_g(int G, const LaunchArgs& a, const AttnPlan& p, char* ws) {
   switch (G) {
-    case 1: LV_ROWS(1); return LV_OK;
-    case 2: LV_ROWS(2); return LV_OK;
-    case 4: LV_ROWS(4); return LV_OK;
-    case 8: LV_ROWS(8); return LV_OK;
+    case 1: launch<T, D, 1, BS>(a, p, ws); return LV_OK;
+    case 2: launch<T, D, 2, BS>(a, p, ws); return LV_OK;
+    case 4: launch<T, D, 4, BS>(a, p, ws); return LV_OK;
+    case 8: launch<T, D, 8, BS>(a, p, ws); return LV_OK;
     default:
       set_error("lv_paged_attention: num_heads/num_kv_heads=%d not in {1,2,4,8}", G);
       return LV_ERR_UNSUPPORTED;
   }
-#undef LV_ROWS
 }
 
 template <typename T>
-static int dispatch_d(int D, int G, int BS, const void* q, int64_t q_stride, const void* kc,
-                      const void* vc, int num_kv_heads, int64_t num_cache_blocks, const int32_t* bt,
-                      int max_blocks, const int32_t* cu, int num_seqs, const int32_t* ctx,
-                      int row_begin, int n_rows, int part_tokens, int max_parts, float scale_log2,
-                      void* out, int64_t out_stride, float* ws_acc, float* ws_ml,
-                      hipStream_t st) {
+static int dispatch_d(int D, int G, int BS, const LaunchArgs& a, const AttnPlan& p, char* ws) {
   if (BS != 16) {
     set_error("lv_paged_attention: block_size=%d unsupported (16)", BS);
     return LV_ERR_UNSUPPORTED;
   }
-  if (D == 128)
-    return dispatch_g<T, 128, 16>(G, q, q_stride, kc, vc, num_kv_heads, num_cache_blocks, bt,
-                                  max_blocks, cu, num_seqs, ctx, row_begin, n_rows, part_tokens,
-                                  max_parts, scale_log2, out, out_stride, ws_acc, ws_ml, st);
-  if (D == 64)
-    return dispatch_g<T, 64, 16>(G, q, q_stride, kc, vc, num_kv_heads, num_cache_blocks, bt,
-                                 max_blocks, cu, num_seqs, ctx, row_begin, n_rows, part_tokens,
-                                 max_parts, scale_log2, out, out_stride, ws_acc, ws_ml, st);
+  if (D == 128) return dispatch_g<T, 128, 16>(G, a, p, ws);
+  if (D == 64) return dispatch_g<T, 64, 16>(G, a, p, ws);
   set_error("lv_paged_attention: head_dim=%d unsupported (64, 128)", D);
   return LV_ERR_UNSUPPORTED;
+}
+
+static int dispatch(lv_dtype dt, int D, int G, int BS, const LaunchArgs& a, const AttnPlan& p,
+                    char* ws) {
+  switch (dt) {
+    case LV_BF16: return dispatch_d<bf16>(D, G, BS, a, p, ws);
+    case LV_F16: return dispatch_d<f16>(D, G, BS, a, p, ws);
+    default: return dispatch_d<float>(D, G, BS, a, p, ws);
+  }
 }
 
 }  // namespace lv
@@ -384,9 +737,14 @@ extern "C" size_t lv_paged_attention_workspace_size(int32_t num_seqs, int32_t nu
                                                     int32_t max_blocks, int32_t max_query_len,
                                                     lv_dtype dtype) {
   (void)num_seqs; (void)num_tokens; (void)max_query_len; (void)dtype;
-  if (num_decodes <= 0 || block_size <= 0 || max_blocks <= 0) return 0;
-  const lv::AttnPlan p = lv::plan_decode(num_decodes, num_heads, head_dim, block_size, max_blocks);
-  return p.acc_bytes + p.ml_bytes;
+  if (num_decodes <= 0 || block_size <= 0 || max_blocks <= 0 || num_heads <= 0) return 0;
+  // num_kv_heads is not an argument: take the larger of the persistent plan
+  // at its biggest grid (one kv head) and the workgroup-per-row plan (used
+  // above kPersistMaxWaves kv heads).
+  const lv::AttnPlan a = lv::plan_decode(num_decodes, num_heads, 1, head_dim, block_size, max_blocks);
+  const lv::AttnPlan b = lv::plan_decode(num_decodes, num_heads, lv::kPersistMaxWaves + 1, head_dim,
+                                         block_size, max_blocks);
+  return a.bytes() > b.bytes() ? a.bytes() : b.bytes();
 }
 
 extern "C" int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
@@ -429,58 +787,40 @@ extern "C" int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
 
   const int G = num_heads / num_kv_heads;
   const float scale_log2 = scale * 0x1.715476p+0f;
-  hipStream_t st = (hipStream_t)stream;
-  int rc = LV_OK;
-
-  auto run = [&](int row_begin, int n_rows, const int32_t* cu, int part_tokens, int max_parts,
-                 float* ws_acc, float* ws_ml) -> int {
-    switch (dtype) {
-      case LV_BF16:
-        return dispatch_d<bf16>(head_dim, G, block_size, query_dev, q_stride_t, key_cache_dev,
-                                value_cache_dev, num_kv_heads, num_cache_blocks, block_tables_dev,
-                                max_blocks, cu, num_seqs, context_lens_dev, row_begin, n_rows,
-                                part_tokens, max_parts, scale_log2, out_dev, out_stride_t, ws_acc,
-                                ws_ml, st);
-      case LV_F16:
-        return dispatch_d<f16>(head_dim, G, block_size, query_dev, q_stride_t, key_cache_dev,
-                               value_cache_dev, num_kv_heads, num_cache_blocks, block_tables_dev,
-                               max_blocks, cu, num_seqs, context_lens_dev, row_begin, n_rows,
-                               part_tokens, max_parts, scale_log2, out_dev, out_stride_t, ws_acc,
-                               ws_ml, st);
-      default:
-        return dispatch_d<float>(head_dim, G, block_size, query_dev, q_stride_t, key_cache_dev,
-                                 value_cache_dev, num_kv_heads, num_cache_blocks, block_tables_dev,
-                                 max_blocks, cu, num_seqs, context_lens_dev, row_begin, n_rows,
-                                 part_tokens, max_parts, scale_log2, out_dev, out_stride_t, ws_acc,
-                                 ws_ml, st);
-    }
-  };
+  LaunchArgs a{query_dev, q_stride_t, key_cache_dev, value_cache_dev, num_kv_heads,
+               num_cache_blocks, block_tables_dev, max_blocks, nullptr, num_seqs,
+               context_lens_dev, 0, 0, scale_log2, out_dev, out_stride_t, (hipStream_t)stream};
 
   if (num_decodes > 0) {
-    const AttnPlan p = plan_decode(num_decodes, num_heads, head_dim, block_size, max_blocks);
-    float* ws_acc = nullptr;
-    float* ws_ml = nullptr;
-    if (p.max_parts > 1) {
-      if (workspace_dev == nullptr || workspace_bytes < p.acc_bytes + p.ml_bytes ||
-          !aligned16(workspace_dev)) {
-        set_error("lv_paged_attention: workspace needs %zu bytes (16-B aligned), got %zu",
-                  p.acc_bytes + p.ml_bytes, workspace_bytes);
-        return LV_ERR_WORKSPACE;
-      }
-      ws_acc = (float*)workspace_dev;
-      ws_ml = (float*)((char*)workspace_dev + p.acc_bytes);
+    const AttnPlan p = plan_decode(num_decodes, num_heads, num_kv_heads, head_dim, block_size,
+                                   max_blocks);
+    if (p.bytes() > 0 && (workspace_dev == nullptr || workspace_bytes < p.bytes() ||
+                          (reinterpret_cast<uintptr_t>(workspace_dev) & 255) != 0)) {
+      set_error("lv_paged_attention: workspace needs %zu bytes (256-B aligned), got %zu",
+                p.bytes(), workspace_bytes);
+      return LV_ERR_WORKSPACE;
     }
     // Decode rows come first, so row i is sequence i: no cu_seqlens lookup.
-    rc = run(0, num_decodes, nullptr, p.part_tokens, p.max_parts, ws_acc, ws_ml);
+    a.cu = nullptr;
+    a.num_seqs = num_decodes;
+    a.row_begin = 0;
+    a.n_rows = num_decodes;
+    const int rc = dispatch(dtype, head_dim, G, block_size, a, p, (char*)workspace_dev);
     if (rc != LV_OK) return rc;
   }
   if (num_decodes < num_seqs) {
     // Prefill-chunk rows: one partition spanning the whole context.
+    AttnPlan p{};
+    p.persistent = false;
+    p.nt = false;
     const int unit = kAttnWaves * block_size;
-    const int pt = ((max_blocks * block_size + unit - 1) / unit) * unit;
-    const int row_begin = num_decodes;
-    const int n_rows = (int)(num_tokens - num_decodes);
-    rc = run(row_begin, n_rows, cu_seqlens_dev, pt, 1, nullptr, nullptr);
+    p.part_tokens = ((max_blocks * block_size + unit - 1) / unit) * unit;
+    p.max_parts = 1;
+    a.cu = cu_seqlens_dev;
+    a.num_seqs = num_seqs;
+    a.row_begin = num_decodes;
+    a.n_rows = (int)(num_tokens - num_decodes);
+    const int rc = dispatch(dtype, head_dim, G, block_size, a, p, nullptr);
     if (rc != LV_OK) return rc;
   }
   return check_launch("lv_paged_attention");

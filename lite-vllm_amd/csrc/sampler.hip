@@ -43,6 +43,7 @@ constexpr int kSampThreads = 1024;
 constexpr int kSampWaves = kSampThreads / 64;
 constexpr int kSeg = 512;
 constexpr int kMaxSegs = 4096;  // vocab up to 2^21
+constexpr int kUnroll = 4;      // segments in flight per wavefront
 
 // log2(e) rounded to fp32.
 constexpr float kLog2e = 0x1.715476p+0f;
@@ -139,20 +140,22 @@ __global__ __launch_bounds__(kSampThreads) void sampler_kernel(
   if (greedy) {
     float bv = -__builtin_inff();
     int64_t bi = INT64_MAX;
-    for (int s = wave; s < nseg; s += 2 * kSampWaves) {
-      float x0[8], x1[8];
-      const int s1 = s + kSampWaves;
-      load_chunk(row, V, s, lane, vec, x0);
-      if (s1 < nseg) load_chunk(row, V, s1, lane, vec, x1);
-      const int64_t e0 = (int64_t)s * kSeg + lane * 8;
+    for (int s0 = wave; s0 < nseg; s0 += kUnroll * kSampWaves) {
+      float x[kUnroll][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (x0[j] > bv) { bv = x0[j]; bi = e0 + j; }
-      if (s1 < nseg) {
-        const int64_t e1 = (int64_t)s1 * kSeg + lane * 8;
+      for (int u = 0; u < kUnroll; ++u) {
+        const int s = s0 + u * kSampWaves;
+        if (s < nseg) load_chunk(row, V, s, lane, vec, x[u]);
+      }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (x1[j] > bv) { bv = x1[j]; bi = e1 + j; }
+      for (int u = 0; u < kUnroll; ++u) {
+        const int s = s0 + u * kSampWaves;
+        if (s < nseg) {
+          const int64_t e0 = (int64_t)s * kSeg + lane * 8;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (x[u][j] > bv) { bv = x[u][j]; bi = e0 + j; }
+        }
       }
     }
     // Lanes may hold their best from a later segment than an equal value of
@@ -174,26 +177,25 @@ __global__ __launch_bounds__(kSampThreads) void sampler_kernel(
   }
 
   // Phase 1: per-segment max and scanned exp weights.
-  for (int s = wave; s < nseg; s += 2 * kSampWaves) {
-    float x0[8], x1[8], e[8];
-    const int s1 = s + kSampWaves;
-    load_chunk(row, V, s, lane, vec, x0);
-    if (s1 < nseg) load_chunk(row, V, s1, lane, vec, x1);
-    {
-      float ms = x0[0];
+  for (int s0 = wave; s0 < nseg; s0 += kUnroll * kSampWaves) {
+    float x[kUnroll][8];
 #pragma unroll
-      for (int j = 1; j < 8; ++j) ms = fmaxf(ms, x0[j]);
-      ms = group_max<64>(ms);
-      const float A = wave_scan_hs(chunk_weights(x0, ms, c, e), lane);
-      if (lane == 63) { s_m[s] = ms; s_w[s] = A; }
+    for (int u = 0; u < kUnroll; ++u) {
+      const int s = s0 + u * kSampWaves;
+      if (s < nseg) load_chunk(row, V, s, lane, vec, x[u]);
     }
-    if (s1 < nseg) {
-      float ms = x1[0];
 #pragma unroll
-      for (int j = 1; j < 8; ++j) ms = fmaxf(ms, x1[j]);
-      ms = group_max<64>(ms);
-      const float A = wave_scan_hs(chunk_weights(x1, ms, c, e), lane);
-      if (lane == 63) { s_m[s1] = ms; s_w[s1] = A; }
+    for (int u = 0; u < kUnroll; ++u) {
+      const int s = s0 + u * kSampWaves;
+      if (s < nseg) {
+        float e[8];
+        float ms = x[u][0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) ms = fmaxf(ms, x[u][j]);
+        ms = group_max<64>(ms);
+        const float A = wave_scan_hs(chunk_weights(x[u], ms, c, e), lane);
+        if (lane == 63) { s_m[s] = ms; s_w[s] = A; }
+      }
     }
   }
   __syncthreads();

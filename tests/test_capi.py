@@ -63,7 +63,10 @@ def test_workspace_size_is_pure_host():
     lib = _hip.load()
     n = lib.lv_paged_attention_workspace_size(256, 256, 256, 16, 128, 16, 128, 1, _hip.LV_BF16)
     assert n > 0 and n % 256 == 0
-    assert lib.lv_paged_attention_workspace_size(4, 4, 4, 16, 128, 16, 1, 1, _hip.LV_BF16) == 0
+    # no decode rows -> no workspace; prefill rows need none
+    assert lib.lv_paged_attention_workspace_size(4, 0, 400, 16, 128, 16, 64, 128, _hip.LV_BF16) == 0
+    small = lib.lv_paged_attention_workspace_size(4, 4, 4, 16, 128, 16, 1, 1, _hip.LV_BF16)
+    assert small > 0 and small % 256 == 0 and small <= n
 
 
 def test_ops_refuse_cpu_tensors():

@@ -140,6 +140,17 @@ def test_decode_config2(device, scaled):
     _check_attention(got, _oracle(batch), f"config2 scaled={scaled}")
 
 
+def test_decode_workspace_reuse_and_counter_reset(device):
+    """Back-to-back calls of different shapes share one workspace; each is
+    correct (stale partials of an earlier call are never read)."""
+    _say("decode workspace reuse")
+    for seed, n, lo, hi in ((21, 300, 1, 3000), (22, 7, 2000, 9000), (23, 64, 1, 40)):
+        batch = workloads.paged_decode(seed=seed, num_seqs=n, ctx_lo=lo, ctx_hi=hi,
+                                       scale_inputs=False)
+        got = _run_attention(batch, device, use_cu=False)
+        _check_attention(got, _oracle(batch), f"reuse seed={seed}")
+
+
 def test_decode_matches_reference_restatement(device):
     """The literal _decode_fast restatement (gather over max_s, mask, einsum)."""
     _say("decode vs literal _decode_fast restatement")
