@@ -516,6 +516,241 @@ __global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
   elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
 }
 
+// ---------------------------------------------------------------------------
+// Prefill-chunk attention on MFMA (bf16 / fp16).
+//
+// One workgroup (4 wavefronts) per (chunk sequence, kv head, tile of 64/G
+// query tokens): its 64 rows are (query token, GQA head) pairs that share one
+// kv head, wavefront w owning rows 16w..16w+15 (row r -> token r % QT,
+// group head r / QT).  Keys stream through LDS in tiles of 32 (two 16-token
+// blocks): K row-major, V transposed.  Per tile and wavefront:
+//   S^T = K Q^T   with v_mfma_f32_16x16x32 (A = K rows from LDS, B = the
+//                 wavefront's Q rows held in registers for the whole kernel);
+//                 lane l then holds query l % 16 against keys 4(l/16)+r and
+//                 16+4(l/16)+r (r = 0..3);
+//   causal mask (key <= query position), online softmax in fp32 (the four
+//   lanes of a query combine their max with two shuffles);
+//   O += P V      with the same instruction: the lane's eight probabilities,
+//                 converted to bf16/fp16, are exactly its A-operand slots once
+//                 the 32-key contraction index is permuted as
+//                 k = 8(l/16) + j -> key (j < 4 ? 4(l/16)+j : 16+4(l/16)+j-4);
+//                 the B operand reads V^T[dim][those keys] as two 8-byte LDS
+//                 loads.
+// K/V for the next tile (and the block ids two tiles ahead) are loaded into
+// registers while the current tile is computed.  Keys at or past the end of
+// the needed range are zero-filled, so they contribute exactly nothing.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16> {
+  using v8 = bf16x8_t;
+  __device__ __forceinline__ static f32x4_t run(v8 a, v8 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static v8 from_bits(const uint4& u) { return __builtin_bit_cast(v8, u); }
+  __device__ __forceinline__ static uint16_t to_bits(float f) { return float_to_bf16_bits(f); }
+};
+template <> struct Mfma<f16> {
+  using v8 = f16x8_t;
+  __device__ __forceinline__ static f32x4_t run(v8 a, v8 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static v8 from_bits(const uint4& u) { return __builtin_bit_cast(v8, u); }
+  __device__ __forceinline__ static uint16_t to_bits(float f) { return float_to_f16_bits(f); }
+};
+
+constexpr int kChunkThreads = 256;
+constexpr int kChunkKeys = 32;
+
+template <typename T, int D, int G, int BS>
+__global__ __launch_bounds__(kChunkThreads) void attn_chunk_mfma_kernel(
+    const T* __restrict__ q, int64_t q_stride,
+    const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
+    const int32_t* __restrict__ block_tables, int max_blocks,
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ ctx, int seq_begin,
+    float scale_log2, T* __restrict__ out, int64_t out_stride) {
+  using M = Mfma<T>;
+  using v8 = typename M::v8;
+  constexpr int QT = 64 / G;            // query tokens per workgroup
+  constexpr int KT = kChunkKeys;        // keys per tile
+  constexpr int KSTEPS = D / 32;        // k-steps of Q K^T
+  constexpr int NTILE = D / 16;         // 16-wide output column tiles
+  constexpr int KROW = D + 8;           // LDS row stride of K (elements)
+  constexpr int VROW = KT + 8;          // LDS row stride of V^T (elements)
+  constexpr int CPR = D / 8;            // 16-byte chunks per key row
+  constexpr int PER_T = KT * CPR / kChunkThreads;  // chunks per thread per tile
+  static_assert(PER_T >= 1 && KT * CPR == PER_T * kChunkThreads, "tile split");
+  static_assert(KT % BS == 0 || BS % KT == 0, "tile / block");
+  __shared__ __align__(16) uint16_t Ks[KT * KROW];
+  __shared__ __align__(16) uint16_t Vt[D * VROW];
+
+  const int seq = seq_begin + (int)blockIdx.z;
+  const int kvh = blockIdx.y;
+  const int q0 = cu[seq];
+  const int qlen = cu[seq + 1] - q0;
+  const int qt0 = (int)blockIdx.x * QT;
+  if (qt0 >= qlen) return;
+  const int ctxlen = min(ctx[seq], max_blocks * BS);
+  const int pos0 = ctxlen - qlen;                        // position of chunk row 0
+  const int kend = max(0, min(ctxlen, pos0 + qt0 + QT));  // keys [0, kend)
+  if (kend <= 0) return;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int lq = lane & 15;        // query index within the wavefront (S^T / P rows)
+  const int lk = lane >> 4;        // k-group of the lane
+  const int64_t tok_stride = (int64_t)num_kv_heads * D;
+  const int32_t* __restrict__ bt = block_tables + (int64_t)seq * max_blocks;
+
+  // Q^T operand: query row (16w + lq) -> (token, head in group).
+  const int row = 16 * wave + lq;
+  const int qtok = qt0 + row % QT;
+  const int qg = row / QT;
+  const int qpos = pos0 + qtok;    // causal limit of this lane's query (S^T layout)
+  v8 qf[KSTEPS];
+  {
+    const T* qp = q + (int64_t)(q0 + min(qtok, qlen - 1)) * q_stride + (int64_t)(kvh * G + qg) * D +
+                  8 * lk;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = M::from_bits(load16(qp + 32 * ks));
+  }
+
+  // Loader: thread chunk c = tid + 256 u -> (key c / CPR, dims 8 (c % CPR) ..).
+  auto block_id = [&](int k) {
+    int b = bt[min(k, kend - 1) / BS];
+    return (b < 0 || b >= num_cache_blocks) ? 0 : b;
+  };
+  auto load_tile = [&](int k0, const int* ids, uint4* kr, uint4* vr) {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int c = threadIdx.x + kChunkThreads * u;
+      const int key = min(k0 + c / CPR, kend - 1);
+      const int64_t off = ((int64_t)ids[u] * BS + key % BS) * tok_stride + (int64_t)kvh * D +
+                          8 * (c % CPR);
+      kr[u] = load16(kc + off);
+      vr[u] = load16(vc + off);
+    }
+  };
+  auto tile_ids = [&](int k0, int* ids) {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u)
+      ids[u] = block_id(k0 + (threadIdx.x + kChunkThreads * u) / CPR);
+  };
+
+  f32x4_t o[NTILE];
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t) o[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = kNegBig, l_run = 0.0f;
+
+  int ids_cur[PER_T], ids_nxt[PER_T];
+  uint4 kcur[PER_T], vcur[PER_T], knx[PER_T], vnx[PER_T];
+  tile_ids(0, ids_cur);
+  load_tile(0, ids_cur, kcur, vcur);
+  tile_ids(KT, ids_nxt);
+
+  for (int k0 = 0; k0 < kend; k0 += KT) {
+    // Next tile's K/V (clamped, always issued) and the ids of the one after.
+    load_tile(k0 + KT, ids_nxt, knx, vnx);
+    int ids_nn[PER_T];
+    tile_ids(k0 + 2 * KT, ids_nn);
+    __builtin_amdgcn_sched_barrier(0);
+
+    __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int c = threadIdx.x + kChunkThreads * u;
+      const int key = c / CPR, d0 = 8 * (c % CPR);
+      const bool live = k0 + key < kend;
+      const uint4 kz = live ? kcur[u] : make_uint4(0, 0, 0, 0);
+      const uint4 vz = live ? vcur[u] : make_uint4(0, 0, 0, 0);
+      store16(&Ks[key * KROW + d0], kz);
+      const uint32_t w[4] = {vz.x, vz.y, vz.z, vz.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        Vt[(d0 + 2 * j) * VROW + key] = (uint16_t)(w[j] & 0xffffu);
+        Vt[(d0 + 2 * j + 1) * VROW + key] = (uint16_t)(w[j] >> 16);
+      }
+    }
+    __syncthreads();
+
+    // S^T = K Q^T for keys k0 .. k0+15 (s0) and k0+16 .. k0+31 (s1).
+    f32x4_t s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const v8 a0 = M::from_bits(*reinterpret_cast<const uint4*>(&Ks[lq * KROW + 32 * ks + 8 * lk]));
+      const v8 a1 =
+          M::from_bits(*reinterpret_cast<const uint4*>(&Ks[(16 + lq) * KROW + 32 * ks + 8 * lk]));
+      s0 = M::run(a0, qf[ks], s0);
+      s1 = M::run(a1, qf[ks], s1);
+    }
+    float sv[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ka = k0 + 4 * lk + r, kb = k0 + 16 + 4 * lk + r;
+      sv[r] = (ka <= qpos && ka < kend) ? s0[r] * scale_log2 : -__builtin_inff();
+      sv[4 + r] = (kb <= qpos && kb < kend) ? s1[r] * scale_log2 : -__builtin_inff();
+    }
+    float mx = sv[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    uint32_t pw[4] = {0u, 0u, 0u, 0u};
+    float psum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float p = fast_exp2(sv[j] - m_new);
+      psum += p;
+      pw[j >> 1] |= (uint32_t)M::to_bits(p) << (16 * (j & 1));
+    }
+    const v8 pa = M::from_bits(make_uint4(pw[0], pw[1], pw[2], pw[3]));
+    l_run = l_run * alpha + psum;
+    // O rows are queries 4 lk + r: fetch their rescale factors.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(alpha, 4 * lk + r);
+#pragma unroll
+      for (int t = 0; t < NTILE; ++t) o[t][r] *= ar;
+    }
+#pragma unroll
+    for (int t = 0; t < NTILE; ++t) {
+      const uint16_t* vrow = &Vt[(16 * t + lq) * VROW];
+      const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * lk);
+      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * lk);
+      o[t] = M::run(pa, M::from_bits(make_uint4(lo.x, lo.y, hi.x, hi.y)), o[t]);
+    }
+
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      kcur[u] = knx[u];
+      vcur[u] = vnx[u];
+      ids_nxt[u] = ids_nn[u];
+    }
+  }
+
+  // Row sums: each query's four lanes hold partial sums of their keys.
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int qi = 4 * lk + r;
+    const float lr = __shfl(l_run, qi);
+    const float inv = lr > 0.0f ? 1.0f / lr : 0.0f;
+    const int orow = 16 * wave + qi;
+    const int otok = qt0 + orow % QT;
+    if (otok < qlen) {
+      T* op = out + (int64_t)(q0 + otok) * out_stride + (int64_t)(kvh * G + orow / QT) * D + lq;
+#pragma unroll
+      for (int t = 0; t < NTILE; ++t) elem<T>::store(op + 16 * t, o[t][r] * inv);
+    }
+  }
+}
+
 // Merge the partitions of one (row, query head); rows with a single
 // partition were finished by the attention kernel.
 template <typename T, int D, int BS>
@@ -729,6 +964,40 @@ static int dispatch(lv_dtype dt, int D, int G, int BS, const LaunchArgs& a, cons
   }
 }
 
+template <typename T, int D, int G>
+static void launch_chunk_kernel(const LaunchArgs& a, const int32_t* cu, int seq_begin, int n_seqs,
+                                int max_query_len) {
+  constexpr int QT = 64 / G;
+  const dim3 grid((max_query_len + QT - 1) / QT, a.num_kv_heads, n_seqs);
+  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16>), grid, dim3(kChunkThreads), 0, a.st,
+                     (const T*)a.q, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.num_kv_heads,
+                     a.num_cache_blocks, a.bt, a.max_blocks, cu, a.ctx, seq_begin, a.scale_log2,
+                     (T*)a.out, a.out_stride);
+}
+
+template <typename T, int D>
+static int launch_chunks_g(int G, const LaunchArgs& a, const int32_t* cu, int seq_begin,
+                           int n_seqs, int max_query_len) {
+  switch (G) {
+    case 1: launch_chunk_kernel<T, D, 1>(a, cu, seq_begin, n_seqs, max_query_len); return LV_OK;
+    case 2: launch_chunk_kernel<T, D, 2>(a, cu, seq_begin, n_seqs, max_query_len); return LV_OK;
+    case 4: launch_chunk_kernel<T, D, 4>(a, cu, seq_begin, n_seqs, max_query_len); return LV_OK;
+    case 8: launch_chunk_kernel<T, D, 8>(a, cu, seq_begin, n_seqs, max_query_len); return LV_OK;
+    default:
+      set_error("lv_paged_attention: num_heads/num_kv_heads=%d not in {1,2,4,8}", G);
+      return LV_ERR_UNSUPPORTED;
+  }
+}
+
+static int launch_chunks(lv_dtype dt, int D, int G, const LaunchArgs& a, const int32_t* cu,
+                         int seq_begin, int n_seqs, int max_query_len) {
+  if (dt == LV_BF16)
+    return D == 128 ? launch_chunks_g<bf16, 128>(G, a, cu, seq_begin, n_seqs, max_query_len)
+                    : launch_chunks_g<bf16, 64>(G, a, cu, seq_begin, n_seqs, max_query_len);
+  return D == 128 ? launch_chunks_g<f16, 128>(G, a, cu, seq_begin, n_seqs, max_query_len)
+                  : launch_chunks_g<f16, 64>(G, a, cu, seq_begin, n_seqs, max_query_len);
+}
+
 }  // namespace lv
 
 extern "C" size_t lv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_decodes,
@@ -808,8 +1077,16 @@ extern "C" int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
     const int rc = dispatch(dtype, head_dim, G, block_size, a, p, (char*)workspace_dev);
     if (rc != LV_OK) return rc;
   }
-  if (num_decodes < num_seqs) {
-    // Prefill-chunk rows: one partition spanning the whole context.
+  if (num_decodes < num_seqs && dtype != LV_F32 && (head_dim == 64 || head_dim == 128) &&
+      block_size == 16 && (G == 1 || G == 2 || G == 4 || G == 8) &&
+      !env_is("LV_ATTN_CHUNK_KERNEL", 'r')) {
+    LV_REQUIRE(max_query_len >= 1, "lv_paged_attention: max_query_len must be >= 1");
+    const int rc = launch_chunks(dtype, head_dim, G, a, cu_seqlens_dev, num_decodes,
+                                 num_seqs - num_decodes, max_query_len);
+    if (rc != LV_OK) return rc;
+  } else if (num_decodes < num_seqs) {
+    // Prefill-chunk rows without an MFMA path (fp32): one row per query
+    // token, one partition spanning the whole context.
     AttnPlan p{};
     p.persistent = false;
     p.nt = false;

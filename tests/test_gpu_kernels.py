@@ -171,6 +171,43 @@ def test_mixed_step_small(device, seed):
     _check_attention(got, _oracle(step.batch), f"mixed small seed={seed}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("heads", [(16, 8, 128), (4, 2, 64), (8, 8, 128), (32, 4, 64), (16, 2, 128)])
+def test_chunks_all_shapes(device, dtype, heads):
+    """Prefill chunks at unaligned offsets (MFMA path for bf16/fp16, per-row
+    path for fp32), mixed with decodes, against the fp32 oracle."""
+    H, Hkv, D = heads
+    _say(f"chunks dtype={dtype} H={H} Hkv={Hkv} D={D}")
+    step = workloads.mixed_step(seed=7, num_decodes=5, dec_lo=1, dec_hi=300, num_chunks=5,
+                                chunk_len=97, off_lo=0, off_hi=400, num_heads=H,
+                                num_kv_heads=Hkv, head_dim=D, num_cache_slots=16 * 300,
+                                dtype=dtype)
+    got = _run_attention(step.batch, device, use_cu=True)
+    _check_attention(got, _oracle(step.batch), f"chunks {dtype} {heads}")
+
+
+def test_chunk_lengths_and_offsets(device):
+    """Chunk lengths 1..70 (ragged last query tile), offsets that are and
+    are not block-aligned, a chunk ending exactly on a block edge."""
+    _say("chunk lengths / offsets")
+    g = torch.Generator().manual_seed(3)
+    for chunk_len, off in ((1, 0), (2, 15), (31, 16), (32, 17), (33, 0), (64, 5), (70, 64), (16, 48)):
+        step = workloads.mixed_step(seed=chunk_len * 100 + off, num_decodes=0, num_chunks=2,
+                                    chunk_len=chunk_len, off_lo=off, off_hi=off,
+                                    num_cache_slots=16 * 64)
+        got = _run_attention(step.batch, device, use_cu=True)
+        _check_attention(got, _oracle(step.batch), f"chunk len={chunk_len} off={off}")
+
+
+def test_mixed_config3_full(device):
+    """The full config-3 step: 192 decodes + 15 chunks of 512 at offsets up
+    to 3072, 200k-slot cache, N(0,1) values."""
+    _say("mixed config3 full")
+    step = workloads.mixed_step(seed=0)
+    got = _run_attention(step.batch, device, use_cu=True)
+    _check_attention(got, _oracle(step.batch), "config3")
+
+
 def test_prefill_only_offset_zero(device):
     _say("prefill only, offset 0")
     step = workloads.mixed_step(seed=4, num_decodes=0, num_chunks=3, chunk_len=100, off_lo=0,
