@@ -1,0 +1,168 @@
+"""LLMEngine: schedule -> one mixed forward -> one fused sampling launch ->
+bookkeeping.
+
+Interface of the reference (engine/llm_engine.py:29-245: initialize,
+add_request, step, has_unfinished, run_to_completion) and the same stop rules
+(EOS, stop_token_ids, max_tokens, stop strings; llm_engine.py:201-229).  A
+step runs ONE forward for the whole scheduled batch (the reference runs one
+for the decodes plus one per prefill group, llm_engine.py:127-138) and
+samples every finished row with one lv_sample call and one device-to-host
+copy (the reference calls Sampler.sample and .item() per sequence,
+llm_engine.py:197).  Text is produced incrementally only when somebody reads
+it (streaming, or the final output).
+"""
+
+from __future__ import annotations
+
+import uuid
+from typing import Optional
+
+import torch
+
+from ..cache.block_manager import BlockManager
+from ..cache.prefix_cache import PrefixCache
+from ..config import EngineConfig, SamplingParams
+from ..layers.sampler import Sampler
+from ..tokenizer import TokenizerGroup, get_tokenizer
+from .model_runner import ModelRunner
+from .scheduler import Scheduler
+from .sequence import Sequence, SequenceGroup, SequenceGroupOutput, SequenceStatus
+
+
+class LLMEngine:
+    def __init__(self, engine_config: EngineConfig) -> None:
+        self.config = engine_config
+        self.tokenizer: Optional[TokenizerGroup] = None
+        self.model_runner: Optional[ModelRunner] = None
+        self.scheduler: Optional[Scheduler] = None
+        self.block_manager: Optional[BlockManager] = None
+        self.prefix_cache: Optional[PrefixCache] = None
+        self.sampler = Sampler()
+        self.stream_text = False   # AsyncLLM turns this on to get per-step deltas
+        self._rng: Optional[torch.Generator] = None
+
+    def initialize(self) -> None:
+        self.config.resolve()
+        mc = self.config.model_config
+        if not self.config.skip_tokenizer_init:
+            self.tokenizer = get_tokenizer(mc.model, mc.trust_remote_code, mc.revision)
+        self.model_runner = ModelRunner(self.config)
+        self.model_runner.load_model()
+        cc = self.config.cache_config
+        if cc.num_gpu_blocks is None:
+            cc.num_gpu_blocks = self.model_runner.profile_num_gpu_blocks()
+        self.model_runner.init_kv_cache(cc.num_gpu_blocks)
+        self.block_manager = BlockManager(cc.block_size, cc.num_gpu_blocks, cc.num_cpu_blocks)
+        if cc.enable_prefix_caching:
+            self.prefix_cache = PrefixCache(cc.block_size, self.block_manager)
+        self.scheduler = Scheduler(self.config.scheduler_config, cc, self.block_manager,
+                                   self.prefix_cache)
+        dev = torch.device(self.config.device)
+        self._rng = torch.Generator(device=dev)
+        self._rng.manual_seed(self.config.seed)
+
+    # ------------------------------------------------------------------
+    def add_request(self, prompt: Optional[str], sampling_params: SamplingParams,
+                    request_id: Optional[str] = None,
+                    prompt_token_ids: Optional[list[int]] = None) -> str:
+        if request_id is None:
+            request_id = str(uuid.uuid4())
+        if prompt_token_ids is None:
+            if self.tokenizer is None:
+                raise ValueError("no tokenizer: pass prompt_token_ids")
+            prompt_token_ids = self.tokenizer.encode(prompt)
+        if not prompt_token_ids:
+            raise ValueError("empty prompt")
+        sg = SequenceGroup.create(request_id, prompt_token_ids, sampling_params,
+                                  prompt_text=prompt or "")
+        self.scheduler.add_request(sg)
+        return request_id
+
+    def has_unfinished(self) -> bool:
+        return self.scheduler.has_unfinished()
+
+    def step(self) -> list[SequenceGroupOutput]:
+        sched = self.scheduler.schedule()
+        if sched.is_empty:
+            return []
+        meta = self.model_runner.prepare_inputs(sched.scheduled_seq_groups, self.block_manager)
+        # the forward runs even when no row is sampled: a chunk that does not
+        # finish its prompt still has to write its K/V
+        logits = self.model_runner.execute_model(meta)
+        tokens = self._sample(logits, meta) if meta.sample_seqs else []
+
+        sampled = {seq.seq_id: tok for seq, tok in zip(meta.sample_seqs, tokens)}
+        for sg in sched.scheduled_seq_groups:
+            for seq in sg.get_unfinished_seqs():
+                was_prefill = seq.is_prefill
+                if was_prefill:
+                    seq.num_computed_tokens += seq.num_scheduled_tokens or \
+                        (seq.data.prompt_len - seq.num_computed_tokens)
+                    if self.prefix_cache is not None:
+                        self.prefix_cache.insert(
+                            seq.data.prompt_token_ids[:seq.num_computed_tokens],
+                            self.block_manager.get_block_table(seq.seq_id))
+                else:
+                    seq.num_computed_tokens = seq.data.total_len
+                seq.num_scheduled_tokens = 0
+                tok = sampled.get(seq.seq_id)
+                if tok is not None:
+                    seq.data.append_token(tok)
+                    self._check_stop(seq, sg.sampling_params, tok)
+
+        outputs = [self._build_step_output(sg) for sg in sched.scheduled_seq_groups]
+        self.scheduler.update_running(sched.scheduled_seq_groups)
+        self.scheduler.free_finished()
+        return outputs
+
+    def run_to_completion(self) -> list[SequenceGroupOutput]:
+        finished: list[SequenceGroupOutput] = []
+        while self.has_unfinished():
+            for out in self.step():
+                if out.finished:
+                    finished.append(out)
+        return finished
+
+    # ------------------------------------------------------------------
+    def _sample(self, logits: torch.Tensor, meta) -> list[int]:
+        groups = meta.sample_groups
+        simple = all(sg.sampling_params.top_k <= 0 and sg.sampling_params.top_p >= 1.0
+                     for sg in groups)
+        if simple:
+            dev = logits.device
+            temps = torch.tensor([sg.sampling_params.temperature for sg in groups],
+                                 dtype=torch.float32).to(dev, non_blocking=True)
+            uni = torch.rand(len(groups), dtype=torch.float32, device=dev, generator=self._rng)
+            return self.sampler.sample_batched(logits, temps, uni).tolist()
+        out = [self.sampler.sample(logits[i], sg.sampling_params, generator=self._rng)
+               for i, sg in enumerate(groups)]
+        return torch.cat(out).tolist()
+
+    def _check_stop(self, seq: Sequence, params: SamplingParams, token_id: int) -> None:
+        eos = self.tokenizer.eos_token_id if self.tokenizer is not None else None
+        if not params.ignore_eos and eos is not None and token_id == eos:
+            seq.status = SequenceStatus.FINISHED_EOS
+        elif token_id in params.stop_token_ids:
+            seq.status = SequenceStatus.FINISHED_STOPPED
+        elif seq.data.output_len >= params.max_tokens:
+            seq.status = SequenceStatus.FINISHED_LENGTH
+        elif params.stop and self.tokenizer is not None:
+            text = self.tokenizer.decode(seq.data.output_token_ids, skip_special_tokens=False)
+            if any(s in text for s in params.stop):
+                seq.status = SequenceStatus.FINISHED_STOPPED
+
+    def _build_step_output(self, sg: SequenceGroup) -> SequenceGroupOutput:
+        seq = sg.seqs[0]
+        finished = sg.is_finished
+        text, delta = seq.emitted_text, ""
+        if self.tokenizer is not None and (finished or self.stream_text):
+            text = self.tokenizer.decode(seq.data.output_token_ids,
+                                         skip_special_tokens=sg.sampling_params.skip_special_tokens)
+            delta = text[len(seq.emitted_text):]
+            seq.emitted_text = text
+        return SequenceGroupOutput(request_id=sg.request_id, prompt_text=sg.prompt_text,
+                                   prompt_token_ids=seq.data.prompt_token_ids,
+                                   output_token_ids=list(seq.data.output_token_ids)
+                                   if finished else seq.data.output_token_ids,
+                                   output_text=text, finish_reason=seq.status.value,
+                                   delta_text=delta, finished=finished)
