@@ -1,12 +1,17 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X continuous-batching hot path (one GPU).
 
-Default workload (``--workload decode``): paged decode attention at the
-Qwen3-0.6B attention shape, 256 sequences, context U[128, 2048], 16 q / 8 kv
-heads, head_dim 128, block_size 16, bf16 (fp32 accumulate).  One "step" is
-one lv_paged_attention call over the whole batch with every input resident
-in HBM.  Other workloads: ``mixed`` (chunked-prefill step: pack + scatter +
-attention), ``sampler`` (fused sampler on [256, 151936] bf16 logits).
+Default workload (``--workload e2e``): LLM.generate over 256 requests on a
+random-init Qwen3-0.6B-shaped model in bf16 (prompts U[100,1024], half of
+them behind a shared 512-token prefix with prefix caching on, 1024 greedy
+output tokens each, ignore EOS); value = output tokens/s, one "step" = one
+generate() over the whole workload.  Its roofline is the decode-attention
+kernel measured live inside that run; the config-2 microbench of the same
+kernel is reported beside it.  Kernel workloads: ``decode`` (paged decode
+attention at the Qwen3-0.6B attention shape, 256 sequences, context
+U[128, 2048], one lv_paged_attention call per step), ``mixed``
+(chunked-prefill step: pack + scatter + attention), ``sampler`` (fused
+sampler on [256, 151936] bf16 logits), ``copy`` (counter calibration).
 
 Prints ONE JSON line with the throughput, the roofline of the dominant
 kernel (algorithmic bytes / average duration measured with HIP events on
@@ -32,6 +37,10 @@ for p in (str(ROOT), str(ROOT / "lite-vllm_amd")):
 METRIC = "output tok/s (Qwen3-0.6B shape, 256 seqs, 1 GPU); paged-decode attn HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def _cpu_threads() -> int:
@@ -242,6 +251,159 @@ def bench_mixed(args):
     }
 
 
+def bench_e2e(args):
+    """Config 5: LLM.generate over 256 Qwen3-0.6B-shaped requests (random
+    init, bf16), prefix caching on, 8192-token step budget, chunk 512.  One
+    step = one generate() of the whole workload; value = output tokens / wall
+    time.  The decode-attention launches of decode-only steps are bracketed
+    by HIP events on the launch stream for the roofline."""
+    import torch
+    from litevllm import LLM, SamplingParams, ops, workloads
+    from litevllm.engine import model_runner as mr
+
+    mc = workloads.QWEN3_06B_SHAPE
+    prompts, sharers = workloads.e2e_prompts(seed=0)
+    warm_prompts, _ = workloads.e2e_prompts(seed=1)
+    llm = LLM("qwen3-0.6b-shape", dtype="bfloat16", load_format="dummy", hf_overrides=mc,
+              skip_tokenizer_init=True, enable_prefix_caching=True, max_num_batched_tokens=8192,
+              chunk_size=512, block_size=16, max_num_seqs=256, seed=0)
+    eng = llm.engine
+    sp = SamplingParams(temperature=0.0, max_tokens=args.output_len, ignore_eos=True)
+
+    # -- instrumentation: events around decode attention in decode-only steps
+    probe = {"on": False, "meta": None, "events": [], "bytes": 0}
+    hkv, D, H = mc["num_key_value_heads"], mc["head_dim"], mc["num_attention_heads"]
+    orig_exec = mr.ModelRunner.execute_model
+    orig_attn = ops.paged_attention
+
+    def exec_probe(self, meta):
+        probe["meta"] = meta
+        return orig_exec(self, meta)
+
+    def attn_probe(query, *a, **kw):
+        meta = probe["meta"]
+        if not probe["on"] or meta is None or meta.num_decodes != len(meta.seq_ids):
+            return orig_attn(query, *a, **kw)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        out = orig_attn(query, *a, **kw)
+        e1.record()
+        B = meta.num_decodes
+        probe["events"].append((e0, e1))
+        probe["bytes"] += (meta.num_context_tokens * hkv * D * 2 * 2 + 2 * B * H * D * 2
+                           + meta.num_context_blocks * 4 + B * 4)
+        return out
+
+    mr.ModelRunner.execute_model = exec_probe
+    ops.paged_attention = attn_probe
+
+    def reset_prefix_cache():
+        pc = eng.prefix_cache
+        pc.evict_unused(len(pc.cache))
+
+    warm_sp = SamplingParams(temperature=0.0, max_tokens=8, ignore_eos=True)
+    _log("e2e: model and KV cache ready")
+    for _ in range(args.warmup):
+        llm.generate(prompt_token_ids=warm_prompts, sampling_params=warm_sp)
+        reset_prefix_cache()
+        _log("e2e: warmup generate done")
+    torch.cuda.synchronize()
+    probe["on"] = True
+    hits0 = eng.prefix_cache.hit_tokens
+    t0 = time.perf_counter()
+    n_out = 0
+    for i in range(args.steps):
+        outs = llm.generate(prompt_token_ids=prompts, sampling_params=sp)
+        n_out += sum(o.num_output_tokens for o in outs)
+        _log(f"e2e: timed generate {i + 1}/{args.steps} done")
+        if i + 1 < args.steps:
+            reset_prefix_cache()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    probe["on"] = False
+    mr.ModelRunner.execute_model = orig_exec
+    ops.paged_attention = orig_attn
+    durs = [a.elapsed_time(b) for a, b in probe["events"]]
+    cpu_state = cpu_cfg = None
+    if not args.no_cpu_baseline:
+        cpu_state = {k: v.detach().to("cpu", torch.float32)
+                     for k, v in eng.model_runner.model.state_dict().items()}
+        cpu_cfg = eng.config.model_config
+    attn_ms = sum(durs)
+    achieved = probe["bytes"] / (attn_ms * 1e-3) / 1e9 if durs else 0.0
+    result = {
+        "value": round(n_out / wall, 1), "unit": "output tok/s",
+        "ms_per_step": round(wall * 1e3 / args.steps, 2),
+        "config": {
+            "workload": "config5 e2e: LLM.generate, Qwen3-0.6B shape (28 layers, hidden 1024, "
+                        "MLP 3072, 16q/8kv, D128, qk-norm, theta 1e6, vocab 151936, untied), "
+                        "random init seed 0, bf16; 256 prompts U[100,1024] (128 share a 512-token "
+                        "prefix, length max(drawn,528)), prefix caching on, "
+                        f"{args.output_len} output tokens ignore_eos, greedy, "
+                        "max_num_batched_tokens 8192, chunk 512, block 16",
+            "num_seqs": len(prompts), "prompt_tokens": sum(map(len, prompts)),
+            "output_tokens": n_out, "prefix_hit_tokens": eng.prefix_cache.hit_tokens - hits0,
+            "num_gpu_blocks": eng.config.cache_config.num_gpu_blocks,
+            "kernel": "lv_paged_attention decode (attn_decode_persistent_kernel + "
+                      "attn_persist_reduce_kernel), decode-only steps",
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": _traffic("e2e_decode"),
+            "algorithmic_bytes": int(probe["bytes"] / max(len(durs), 1)),
+            "avg_launch_us": round(attn_ms * 1e3 / max(len(durs), 1), 2),
+            "launches": len(durs), "attention_share_of_wall": round(attn_ms * 1e-3 / wall, 4),
+        },
+    }
+    del llm, eng
+    torch.cuda.empty_cache()
+    if args.no_secondary:
+        if not args.no_cpu_baseline:
+            result["cpu_baseline"] = cpu_baseline_e2e(cpu_state, cpu_cfg, prompts)
+        return result
+    _log("e2e: config-2 decode-attention microbench")
+    dec = bench_decode(argparse.Namespace(steps=50, warmup=10, no_cpu_baseline=True))
+    result["secondary"] = {
+        "metric": "paged-decode attn HBM GB/s (config 2, 50 launches after 10 warmup)",
+        "value": dec["value"], "unit": dec["unit"], "roofline": dec["roofline"],
+        "config": dec["config"]["workload"]}
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_e2e(cpu_state, cpu_cfg, prompts)
+    return result
+
+
+def cpu_baseline_e2e(state, model_config, prompts, n_seqs: int = 8, n_steps: int = 4):
+    """The reference's CPU model path restated (oracle.model, fp32, the same
+    random weights): prefill the first n_seqs prompts of the workload
+    (untimed), then time n_steps batched greedy decode steps."""
+    import torch
+    from oracle.model import OracleDecoder
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    o = OracleDecoder(state, model_config, use_qk_norm=True)
+    kvs, toks, pos = [], [], []
+    for p in prompts[:n_seqs]:
+        kv: list = []
+        toks.append(int(torch.argmax(o.forward(p, 0, kv))))
+        kvs.append(kv)
+        pos.append(len(p))
+    _log("e2e cpu baseline: prefill done")
+    t0 = time.perf_counter()
+    for _ in range(n_steps):
+        logits = o.decode_batch(toks, pos, kvs)
+        toks = logits.argmax(-1).tolist()
+        pos = [x + 1 for x in pos]
+    secs = time.perf_counter() - t0
+    return {"value": round(n_seqs * n_steps / secs, 2), "unit": "output tok/s",
+            "cores": threads, "kind": "port",
+            "sample": f"config5 prompts 0..{n_seqs - 1} ({sum(map(len, prompts[:n_seqs]))} prompt "
+                      f"tokens, prefill untimed), {n_steps} batched greedy decode steps of "
+                      f"oracle.model.OracleDecoder (fp32 restatement of the reference model "
+                      f"path): {secs:.2f} s"}
+
+
 def bench_copy(args):
     """Plain device copy of 1 GiB (torch copy_): the calibration kernel for
     the HBM byte counters and the achievable-bandwidth reference."""
@@ -265,11 +427,25 @@ def bench_copy(args):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "sampler", "mixed", "copy"], default="decode")
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 1 for e2e, 50 for the kernel workloads)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps (default: 1 for e2e, 10 otherwise)")
+    ap.add_argument("--workload", choices=["e2e", "decode", "sampler", "mixed", "copy"],
+                    default="e2e")
+    ap.add_argument("--output-len", type=int, default=1024,
+                    help="e2e: output tokens per request")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="e2e: skip the config-2 decode-attention microbench")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 1 if args.workload == "e2e" else 50
+    if args.warmup is None:
+        args.warmup = 1 if args.workload == "e2e" else 10
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus "
               f"{args.gpus}", file=sys.stderr)
@@ -278,7 +454,7 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
-    fn = {"decode": bench_decode, "sampler": bench_sampler, "mixed": bench_mixed,
+    fn = {"e2e": bench_e2e, "decode": bench_decode, "sampler": bench_sampler, "mixed": bench_mixed,
           "copy": bench_copy}[args.workload]
     res = fn(args)
     line = {
@@ -287,7 +463,7 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded torch.Generator, seed 0)", "config": res["config"],
     }
-    for k in ("roofline", "cpu_baseline"):
+    for k in ("roofline", "cpu_baseline", "secondary"):
         if k in res:
             line[k] = res[k]
     print(json.dumps(line), flush=True)

@@ -204,6 +204,59 @@ int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
               const float* uniform_dev, int64_t* out_ids_dev, lv_dtype dtype,
               void* stream);
 
+/* ------------------------------------------------------------------------
+ * Fused layer prologue / epilogue work (the elementwise ops the reference
+ * runs as separate torch ops around its GEMMs).  Rounding follows the
+ * reference op by op: each intermediate the reference materialises in the
+ * model dtype is rounded to that dtype.  The fp32 sum of squares is reduced
+ * in a different order than torch's, so results agree within 1-2 ulp of the
+ * dtype, not bit for bit.
+ * ---------------------------------------------------------------------- */
+
+/* Residual add + RMSNorm.  Replaces LlamaRMSNorm.forward
+ * (litevllm/models/llama.py:24-27) together with the residual adds of the
+ * decoder layer (models/qwen3.py:131-140, llama.py:133-142):
+ *   if residual != NULL:  residual[t] = x[t] + residual[t];  src = residual[t]
+ *   else                  src = x[t]
+ *   out[t] = weight * to_dtype(src * rsqrt(mean(src^2) + eps))
+ * Rows are [num_tokens, hidden] with the given element strides; every row
+ * must start on a 16-byte boundary and hidden must be a multiple of 16 bytes
+ * worth of elements.  out may not alias x or residual. */
+int lv_add_rms_norm(const void* x_dev, int64_t x_stride_t, void* residual_dev,
+                    int64_t residual_stride_t, const void* weight_dev, void* out_dev,
+                    int64_t out_stride_t, int64_t num_tokens, int32_t hidden, float eps,
+                    lv_dtype dtype, void* stream);
+
+/* Attention prologue of one layer.  Replaces, for a fused q|k|v projection
+ * row qkv[t] = [q (H*D) | k (Hkv*D) | v (Hkv*D)], the sequence
+ * q_norm/k_norm (models/qwen3.py:75-77; pass NULL weights for Llama),
+ * rotary_emb + apply_rotary_emb (layers/rotary_emb.py:92-117, with the
+ * module's cos/sin caches, [max_position, D/2] in the model dtype) and the
+ * K/V cache write (layers/attention.py:79-84, PagedAttention.write_to_cache
+ * attention.py:17-33):
+ *   q_out[t, h]                     = rope(norm_q(q[t, h]), positions[t])
+ *   key_cache  row slot_mapping[t]  = rope(norm_k(k[t]), positions[t])
+ *   value_cache row slot_mapping[t] = v[t]
+ * Tokens with slot < 0 (padding) or slot >= num_blocks*block_size write no
+ * cache row; a position outside [0, max_position) yields NaN rows.
+ * head_dim in {64, 128, 256}. */
+int lv_qk_norm_rope_cache(const void* qkv_dev, int64_t qkv_stride_t,
+                          const void* q_norm_weight_dev, const void* k_norm_weight_dev,
+                          const void* cos_dev, const void* sin_dev, int64_t max_position,
+                          const int64_t* positions_dev, const int64_t* slot_mapping_dev,
+                          void* q_out_dev, int64_t q_out_stride_t, void* key_cache_dev,
+                          void* value_cache_dev, int64_t num_blocks, int32_t block_size,
+                          int64_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                          int32_t head_dim, float eps, lv_dtype dtype, void* stream);
+
+/* Gated-MLP activation.  Replaces F.silu(gate) * up of LlamaMLP.forward
+ * (models/llama.py:37-38) for a fused gate|up row:
+ *   out[t, i] = to_dtype(silu(gate_up[t, i])) * gate_up[t, intermediate + i]
+ * Rows 16-byte aligned; intermediate a multiple of 16 bytes of elements. */
+int lv_silu_mul(const void* gate_up_dev, int64_t in_stride_t, void* out_dev,
+                int64_t out_stride_t, int64_t num_tokens, int32_t intermediate,
+                lv_dtype dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -97,6 +97,38 @@ template <> struct elem<f16> {
   __device__ __forceinline__ static void store(f16* p, float v) { p->bits = float_to_f16_bits(v); }
 };
 
+// Value after a store to T and a reload (fp32 arithmetic rounded to the
+// storage type, the way a torch op with a T-typed output rounds).
+template <typename T> __device__ __forceinline__ float round_to(float v);
+template <> __device__ __forceinline__ float round_to<float>(float v) { return v; }
+template <> __device__ __forceinline__ float round_to<bf16>(float v) {
+  return bf16_bits_to_float(float_to_bf16_bits(v));
+}
+template <> __device__ __forceinline__ float round_to<f16>(float v) {
+  return f16_bits_to_float(float_to_f16_bits(v));
+}
+
+// Pack kPer16B fp32 values (already representable in T) into 16 bytes.
+template <typename T> __device__ __forceinline__ uint4 pack16(const float* v);
+template <> __device__ __forceinline__ uint4 pack16<float>(const float* v) {
+  return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                    __float_as_uint(v[3]));
+}
+template <> __device__ __forceinline__ uint4 pack16<bf16>(const float* v) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)float_to_bf16_bits(v[2 * i]) | ((uint32_t)float_to_bf16_bits(v[2 * i + 1]) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+template <> __device__ __forceinline__ uint4 pack16<f16>(const float* v) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)float_to_f16_bits(v[2 * i]) | ((uint32_t)float_to_f16_bits(v[2 * i + 1]) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }

@@ -44,6 +44,8 @@ COMMON_FLAGS = [
 # it bit for bit.
 EXTRA_FLAGS = {
     "sampler.hip": ["-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt"],
+    # products and sums rounded separately, as the reference's separate ops do
+    "fused_layers.hip": ["-ffp-contract=off"],
 }
 
 

@@ -64,6 +64,26 @@ SIGNATURES: dict[str, tuple] = {
         _c_p, _c_p, _c_p,              # temperature, uniform, out_ids
         ctypes.c_int, _c_p,            # dtype, stream
     ]),
+    "lv_add_rms_norm": (ctypes.c_int, [
+        _c_p, _c_i64, _c_p, _c_i64,    # x, x_stride, residual, residual_stride
+        _c_p, _c_p, _c_i64,            # weight, out, out_stride
+        _c_i64, _c_i32, ctypes.c_float,  # num_tokens, hidden, eps
+        ctypes.c_int, _c_p,            # dtype, stream
+    ]),
+    "lv_qk_norm_rope_cache": (ctypes.c_int, [
+        _c_p, _c_i64, _c_p, _c_p,      # qkv, qkv_stride, q_norm_w, k_norm_w
+        _c_p, _c_p, _c_i64,            # cos, sin, max_position
+        _c_p, _c_p,                    # positions, slot_mapping
+        _c_p, _c_i64, _c_p, _c_p,      # q_out, q_out_stride, key_cache, value_cache
+        _c_i64, _c_i32, _c_i64,        # num_blocks, block_size, num_tokens
+        _c_i32, _c_i32, _c_i32,        # num_heads, num_kv_heads, head_dim
+        ctypes.c_float, ctypes.c_int, _c_p,  # eps, dtype, stream
+    ]),
+    "lv_silu_mul": (ctypes.c_int, [
+        _c_p, _c_i64, _c_p, _c_i64,    # gate_up, in_stride, out, out_stride
+        _c_i64, _c_i32,                # num_tokens, intermediate
+        ctypes.c_int, _c_p,            # dtype, stream
+    ]),
 }
 
 _lock = threading.Lock()

@@ -69,7 +69,9 @@ class InputMetadata:
                  is_prefill, seq_ids, attn_metadata: Optional[AttentionMetadata] = None,
                  logits_indices: Optional[torch.Tensor] = None,
                  sample_seqs: Optional[list[Sequence]] = None,
-                 sample_groups: Optional[list[SequenceGroup]] = None) -> None:
+                 sample_groups: Optional[list[SequenceGroup]] = None,
+                 num_decodes: int = 0, num_context_tokens: int = 0,
+                 num_context_blocks: int = 0) -> None:
         self.input_ids = input_ids
         self.positions = positions
         self.slot_mapping = slot_mapping
@@ -81,6 +83,9 @@ class InputMetadata:
         self.logits_indices = logits_indices
         self.sample_seqs = sample_seqs or []
         self.sample_groups = sample_groups or []
+        self.num_decodes = num_decodes                 # leading 1-token sequences
+        self.num_context_tokens = num_context_tokens   # sum of context lengths (host)
+        self.num_context_blocks = num_context_blocks   # sum of block-table lengths (host)
 
 
 @dataclass
@@ -236,7 +241,10 @@ class ModelRunner:
         return InputMetadata(packed["input_ids"], packed["positions"], packed["slot_mapping"],
                              packed["block_tables"], packed["context_lens"], st.is_prefill,
                              st.seq_ids, attn_metadata=attn, logits_indices=d64[n_tok:],
-                             sample_seqs=st.sample_seqs, sample_groups=st.sample_groups)
+                             sample_seqs=st.sample_seqs, sample_groups=st.sample_groups,
+                             num_decodes=st.num_decodes,
+                             num_context_tokens=int(st.descs[:, 0].sum() + st.descs[:, 1].sum()),
+                             num_context_blocks=int(n_blocks))
 
     @torch.inference_mode()
     def execute_model(self, metadata: InputMetadata) -> torch.Tensor:

@@ -9,8 +9,8 @@ from typing import Optional
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
+from litevllm import ops
 from litevllm.config import ModelConfig
 from litevllm.layers.attention import Attention
 from litevllm.layers.rotary_emb import RotaryEmbedding, apply_rotary_emb
@@ -18,17 +18,24 @@ from litevllm.models.base import BaseModelForCausalLM
 
 
 class RMSNorm(nn.Module):
-    """fp32 variance, scale applied in the weight dtype (reference llama.py:18-27)."""
+    """RMSNorm with the reference's rounding (fp32 statistics, normalised
+    value cast to the weight dtype, then scaled; reference llama.py:18-27),
+    run by lv_add_rms_norm.  With `residual`, the residual add of the decoder
+    layer is fused in: residual += x (in place), returns (norm(residual),
+    residual)."""
 
     def __init__(self, hidden_size: int, eps: float = 1e-6) -> None:
         super().__init__()
         self.weight = nn.Parameter(torch.ones(hidden_size))
         self.eps = eps
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return self.weight * xf.to(self.weight.dtype)
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None):
+        n = self.weight.shape[0]
+        rows = x.reshape(-1, n)
+        if residual is None:
+            return ops.add_rms_norm(rows, self.weight, self.eps).view(x.shape)
+        out = ops.add_rms_norm(rows, self.weight, self.eps, residual=residual)
+        return out.view(x.shape), residual
 
 
 class GatedMLP(nn.Module):
@@ -41,8 +48,7 @@ class GatedMLP(nn.Module):
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        gate, up = self.gate_up_proj(x).split(self.intermediate_size, dim=-1)
-        return self.down_proj(F.silu(gate) * up)
+        return self.down_proj(ops.silu_mul(self.gate_up_proj(x)))
 
 
 class DecoderAttention(nn.Module):
@@ -71,10 +77,25 @@ class DecoderAttention(nn.Module):
     def forward(self, hidden: torch.Tensor, positions: torch.Tensor, kv_cache, slot_mapping,
                 block_table, context_lens, is_prefill, attn_metadata) -> torch.Tensor:
         T = hidden.shape[0]
-        q, k, v = self.qkv_proj(hidden).split([self.q_size, self.kv_size, self.kv_size], dim=-1)
-        q = q.view(T, self.num_heads, self.head_dim)
-        k = k.view(T, self.num_kv_heads, self.head_dim)
-        v = v.view(T, self.num_kv_heads, self.head_dim)
+        qkv = self.qkv_proj(hidden)
+        if attn_metadata is not None and kv_cache is not None:
+            # engine path: one fused prologue kernel (q/k norm, RoPE, K/V into
+            # the paged cache), then attention over the cache
+            key_cache, value_cache = kv_cache
+            q = ops.qk_norm_rope_cache(
+                qkv, self.num_heads, self.num_kv_heads, self.head_dim,
+                self.rotary_emb.cos_cached, self.rotary_emb.sin_cached, positions, slot_mapping,
+                key_cache, value_cache,
+                q_norm_weight=self.q_norm.weight if self.use_qk_norm else None,
+                k_norm_weight=self.k_norm.weight if self.use_qk_norm else None,
+                eps=self.q_norm.eps if self.use_qk_norm else 1e-6)
+            out = self.attn(q, None, None, key_cache, value_cache, block_table, None,
+                            context_lens, is_prefill, attn_metadata=attn_metadata)
+            return self.o_proj(out.reshape(T, self.q_size))
+        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+        q = q.reshape(T, self.num_heads, self.head_dim)
+        k = k.reshape(T, self.num_kv_heads, self.head_dim)
+        v = v.reshape(T, self.num_kv_heads, self.head_dim)
         if self.use_qk_norm:
             q = self.q_norm(q)
             k = self.k_norm(k)
@@ -95,13 +116,20 @@ class DecoderLayer(nn.Module):
         self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
-    def forward(self, hidden, positions, kv_cache, slot_mapping, block_table, context_lens,
-                is_prefill, attn_metadata):
-        residual = hidden
-        hidden = self.self_attn(self.input_layernorm(hidden), positions, kv_cache, slot_mapping,
-                                block_table, context_lens, is_prefill, attn_metadata)
-        hidden = residual + hidden
-        return hidden + self.mlp(self.post_attention_layernorm(hidden))
+    def forward(self, hidden, residual, positions, kv_cache, slot_mapping, block_table,
+                context_lens, is_prefill, attn_metadata):
+        """Returns (mlp output, residual stream).  The reference's
+        `residual + hidden` adds (qwen3.py:131-140) happen inside the next
+        RMSNorm call, so the residual stream carries the same bf16 sums."""
+        if residual is None:
+            residual = hidden
+            hidden = self.input_layernorm(hidden)
+        else:
+            hidden, residual = self.input_layernorm(hidden, residual)
+        hidden = self.self_attn(hidden, positions, kv_cache, slot_mapping, block_table,
+                                context_lens, is_prefill, attn_metadata)
+        hidden, residual = self.post_attention_layernorm(hidden, residual)
+        return self.mlp(hidden), residual
 
 
 class DecoderModel(nn.Module):
@@ -114,12 +142,16 @@ class DecoderModel(nn.Module):
 
     def forward(self, input_ids, positions, kv_caches, slot_mapping, block_tables, context_lens,
                 is_prefill, attn_metadata):
+        """Returns (last layer's MLP output, residual stream); the final
+        residual add + norm is left to the caller so it can run on the
+        sampled rows only."""
         hidden = self.embed_tokens(input_ids)
+        residual = None
         for i, layer in enumerate(self.layers):
             kv = kv_caches[i] if kv_caches is not None else None
-            hidden = layer(hidden, positions, kv, slot_mapping, block_tables, context_lens,
-                           is_prefill, attn_metadata)
-        return self.norm(hidden)
+            hidden, residual = layer(hidden, residual, positions, kv, slot_mapping, block_tables,
+                                     context_lens, is_prefill, attn_metadata)
+        return hidden, residual
 
 
 class LlamaForCausalLM(BaseModelForCausalLM):
@@ -136,10 +168,12 @@ class LlamaForCausalLM(BaseModelForCausalLM):
 
     def forward(self, input_ids, positions, kv_caches=None, slot_mapping=None, block_tables=None,
                 context_lens=None, is_prefill=True, attn_metadata=None, logits_indices=None):
-        hidden = self.model(input_ids, positions, kv_caches, slot_mapping, block_tables,
-                            context_lens, is_prefill, attn_metadata)
-        if logits_indices is not None:
+        hidden, residual = self.model(input_ids, positions, kv_caches, slot_mapping,
+                                      block_tables, context_lens, is_prefill, attn_metadata)
+        if logits_indices is not None:   # norm and LM head on the sampled rows only
             hidden = hidden.index_select(0, logits_indices)
+            residual = residual.index_select(0, logits_indices)
+        hidden, _ = self.model.norm(hidden, residual)
         return self.lm_head(hidden)
 
     # -- checkpoint loading ------------------------------------------------

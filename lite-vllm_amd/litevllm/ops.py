@@ -274,3 +274,126 @@ def sample(logits: torch.Tensor, temperature: torch.Tensor,
                        _ptr(out), _dtype_code(logits), _stream(dev))
     _hip.check(rc, "lv_sample")
     return out
+
+
+# ---------------------------------------------------------------------------
+# fused layer work: residual add + RMSNorm, attention prologue, SiLU gate
+# ---------------------------------------------------------------------------
+
+def _check_rows(name: str, t: torch.Tensor, width: int, dtype: torch.dtype) -> None:
+    if t.dim() != 2 or t.shape[1] < width or t.stride(1) != 1:
+        raise RuntimeError(f"`{name}` must be [T, >={width}] with unit column stride, got "
+                           f"{tuple(t.shape)} strides {t.stride()}")
+    if t.dtype != dtype:
+        raise RuntimeError(f"`{name}` dtype {t.dtype} != {dtype}")
+
+
+def add_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                 residual: Optional[torch.Tensor] = None,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = weight * to_dtype(s * rsqrt(mean(s^2) + eps)) with s = x, or,
+    when `residual` is given, s = residual := x + residual (updated in place).
+
+    Reference: litevllm/models/llama.py:24-27 (RMSNorm) and the residual adds
+    of the decoder layer (models/qwen3.py:131-140).  x/residual/out: [T, hidden].
+    """
+    dev = x.device
+    for n, t in (("x", x), ("weight", weight), ("residual", residual), ("out", out)):
+        _require_device(n, t, dev)
+    T, hidden = x.shape
+    _check_rows("x", x, hidden, x.dtype)
+    if weight.shape != (hidden,) or not weight.is_contiguous() or weight.dtype != x.dtype:
+        raise RuntimeError(f"`weight` must be a contiguous [{hidden}] {x.dtype} tensor")
+    if residual is not None:
+        _check_rows("residual", residual, hidden, x.dtype)
+        if residual.shape[0] != T:
+            raise RuntimeError("`residual` rows != x rows")
+    if out is None:
+        out = torch.empty((T, hidden), dtype=x.dtype, device=dev)
+    _check_rows("out", out, hidden, x.dtype)
+    if T == 0:
+        return out
+    lib = _hip.load()
+    rc = lib.lv_add_rms_norm(_ptr(x), x.stride(0), _ptr(residual),
+                             residual.stride(0) if residual is not None else 0, _ptr(weight),
+                             _ptr(out), out.stride(0), T, hidden, float(eps), _dtype_code(x),
+                             _stream(dev))
+    _hip.check(rc, "lv_add_rms_norm")
+    return out
+
+
+def qk_norm_rope_cache(qkv: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
+                       cos_cache: torch.Tensor, sin_cache: torch.Tensor,
+                       positions: torch.Tensor, slot_mapping: torch.Tensor,
+                       key_cache: torch.Tensor, value_cache: torch.Tensor,
+                       q_norm_weight: Optional[torch.Tensor] = None,
+                       k_norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                       q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Split a fused q|k|v projection, RMSNorm q and k per head (when the
+    weights are given), rotate both with the module's cos/sin caches, write
+    the query to q_out [T, H, D] and K/V into the paged cache at slot_mapping.
+
+    Reference: models/qwen3.py:75-84, layers/rotary_emb.py:92-117,
+    layers/attention.py:79-84.
+    """
+    dev = qkv.device
+    for n, t in (("qkv", qkv), ("cos_cache", cos_cache), ("sin_cache", sin_cache),
+                 ("positions", positions), ("slot_mapping", slot_mapping),
+                 ("key_cache", key_cache), ("value_cache", value_cache),
+                 ("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight),
+                 ("q_out", q_out)):
+        _require_device(n, t, dev)
+    H, Hkv, D = num_heads, num_kv_heads, head_dim
+    T = qkv.shape[0]
+    _check_rows("qkv", qkv, (H + 2 * Hkv) * D, key_cache.dtype)
+    _check_int("positions", positions, torch.int64, 1)
+    _check_int("slot_mapping", slot_mapping, torch.int64, 1)
+    if positions.shape[0] != T or slot_mapping.shape[0] != T:
+        raise RuntimeError("positions / slot_mapping length != number of tokens")
+    n_blocks, bs, hkv, d = key_cache.shape
+    if (hkv, d) != (Hkv, D) or value_cache.shape != key_cache.shape or \
+            not key_cache.is_contiguous() or not value_cache.is_contiguous():
+        raise RuntimeError(f"caches must be contiguous [N, bs, {Hkv}, {D}] and equal in shape")
+    for n, t in (("cos_cache", cos_cache), ("sin_cache", sin_cache)):
+        if t.dim() != 2 or t.shape[1] != D // 2 or not t.is_contiguous() or t.dtype != qkv.dtype:
+            raise RuntimeError(f"`{n}` must be a contiguous [max_pos, {D // 2}] {qkv.dtype} tensor")
+    for n, t in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if t is not None and (t.shape != (D,) or not t.is_contiguous() or t.dtype != qkv.dtype):
+            raise RuntimeError(f"`{n}` must be a contiguous [{D}] {qkv.dtype} tensor")
+    if q_out is None:
+        q_out = torch.empty((T, H, D), dtype=qkv.dtype, device=dev)
+    if q_out.shape != (T, H, D) or q_out.stride(2) != 1 or q_out.stride(1) != D:
+        raise RuntimeError("`q_out` must be [T, H, D] with contiguous heads")
+    if T == 0:
+        return q_out
+    lib = _hip.load()
+    rc = lib.lv_qk_norm_rope_cache(
+        _ptr(qkv), qkv.stride(0), _ptr(q_norm_weight), _ptr(k_norm_weight), _ptr(cos_cache),
+        _ptr(sin_cache), cos_cache.shape[0], _ptr(positions), _ptr(slot_mapping), _ptr(q_out),
+        q_out.stride(0), _ptr(key_cache), _ptr(value_cache), n_blocks, bs, T, H, Hkv, D,
+        float(eps), _dtype_code(qkv), _stream(dev))
+    _hip.check(rc, "lv_qk_norm_rope_cache")
+    return q_out
+
+
+def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = to_dtype(silu(gate)) * up for gate_up = [gate | up] per row.
+
+    Reference: models/llama.py:37-38.
+    """
+    dev = gate_up.device
+    _require_device("gate_up", gate_up, dev)
+    _require_device("out", out, dev)
+    T, two_i = gate_up.shape
+    inter = two_i // 2
+    _check_rows("gate_up", gate_up, 2 * inter, gate_up.dtype)
+    if out is None:
+        out = torch.empty((T, inter), dtype=gate_up.dtype, device=dev)
+    _check_rows("out", out, inter, gate_up.dtype)
+    if T == 0:
+        return out
+    lib = _hip.load()
+    rc = lib.lv_silu_mul(_ptr(gate_up), gate_up.stride(0), _ptr(out), out.stride(0), T, inter,
+                         _dtype_code(gate_up), _stream(dev))
+    _hip.check(rc, "lv_silu_mul")
+    return out

@@ -179,3 +179,36 @@ def sampler_batch(seed: int = 0, rows: int = 256, vocab: int = 151936, std: floa
     temp[half:] = 0.5 + 0.5 * torch.rand(rows - half, generator=g)
     uni = torch.rand(rows, generator=g)
     return SamplerBatch(x, temp, uni.to(torch.float32), planted)
+
+
+# -- config 5: end-to-end serving -------------------------------------------
+
+QWEN3_06B_SHAPE = dict(
+    model_type="qwen3", vocab_size=151936, hidden_size=1024, num_hidden_layers=28,
+    num_attention_heads=16, num_key_value_heads=8, head_dim=128, intermediate_size=3072,
+    rope_theta=1e6, rms_norm_eps=1e-6, max_position_embeddings=40960,
+    tie_word_embeddings=False)
+
+
+def e2e_prompts(seed: int = 0, num_seqs: int = 256, len_lo: int = 100, len_hi: int = 1024,
+                vocab: int = 151936, shared_len: int = 512, num_shared: int = 128,
+                min_shared_total: int = 528) -> tuple[list[list[int]], list[int]]:
+    """Config 5 prompts: lengths U[len_lo, len_hi], ids U[0, vocab); a seeded
+    choice of num_shared sequences starts with one common shared_len-token
+    prefix, and those get length max(drawn, min_shared_total) so that the
+    prefix is followed by at least one block of their own.  Returns
+    (prompts, indices of the sharing sequences)."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(len_lo, len_hi + 1, (num_seqs,), generator=g).tolist()
+    shared = torch.randint(0, vocab, (shared_len,), generator=g).tolist()
+    sharers = sorted(torch.randperm(num_seqs, generator=g)[:num_shared].tolist())
+    is_sharer = set(sharers)
+    prompts = []
+    for i, n in enumerate(lens):
+        if i in is_sharer:
+            n = max(n, min_shared_total)
+            tail = torch.randint(0, vocab, (n - shared_len,), generator=g).tolist()
+            prompts.append(shared + tail)
+        else:
+            prompts.append(torch.randint(0, vocab, (n,), generator=g).tolist())
+    return prompts, sharers

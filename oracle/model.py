@@ -78,6 +78,45 @@ class OracleDecoder:
         head = w.get("lm_head.weight", w["model.embed_tokens.weight"])
         return (x @ head.t())[0]
 
+    def decode_batch(self, tokens: list[int], positions: list[int], kvs: list[list]) -> torch.Tensor:
+        """One decode step for B sequences at once, the way the reference's
+        CPU path batches decodes (model_runner.py:217-250, attention.py:
+        91-139): projections and MLP over the B rows together, attention per
+        sequence over its own history.  kvs[b] is sequence b's K/V list (as
+        forward builds it); returns the logits [B, V]."""
+        c, w = self.cfg, self.w
+        H, Hkv, D = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        B = len(tokens)
+        pos = torch.tensor(positions)
+        x = w["model.embed_tokens.weight"][torch.tensor(tokens)]
+        for i in range(c.num_hidden_layers):
+            p = f"model.layers.{i}."
+            h = self._rms(x, w[p + "input_layernorm.weight"])
+            q, k, v = (h @ w[p + "self_attn.qkv_proj.weight"].t()).split([H * D, Hkv * D, Hkv * D],
+                                                                          dim=-1)
+            q, k, v = q.view(B, H, D), k.view(B, Hkv, D), v.view(B, Hkv, D)
+            if self.use_qk_norm:
+                q = self._rms(q, w[p + "self_attn.q_norm.weight"])
+                k = self._rms(k, w[p + "self_attn.k_norm.weight"])
+            q, k = self._rope(q, pos), self._rope(k, pos)
+            outs = []
+            for b in range(B):
+                K0, V0 = kvs[b][i]
+                K = torch.cat([K0, k[b:b + 1]])
+                V = torch.cat([V0, v[b:b + 1]])
+                kvs[b][i] = (K, V)
+                Kr = K.repeat_interleave(H // Hkv, dim=1).permute(1, 0, 2)
+                Vr = V.repeat_interleave(H // Hkv, dim=1).permute(1, 0, 2)
+                s = torch.matmul(q[b].unsqueeze(1), Kr.transpose(1, 2)) / math.sqrt(D)
+                outs.append(torch.matmul(F.softmax(s, dim=-1), Vr).reshape(H * D))
+            x = x + torch.stack(outs) @ w[p + "self_attn.o_proj.weight"].t()
+            h = self._rms(x, w[p + "post_attention_layernorm.weight"])
+            g, u = (h @ w[p + "mlp.gate_up_proj.weight"].t()).split(c.intermediate_size, dim=-1)
+            x = x + (F.silu(g) * u) @ w[p + "mlp.down_proj.weight"].t()
+        x = self._rms(x, w["model.norm.weight"])
+        head = w.get("lm_head.weight", w["model.embed_tokens.weight"])
+        return x @ head.t()
+
     def greedy(self, prompt: list[int], n: int) -> tuple[list[int], list[float]]:
         """n greedy tokens; also the top-1 minus top-2 logit margin of each."""
         kv: list = []

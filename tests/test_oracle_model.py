@@ -45,3 +45,21 @@ def test_rms_matches_torch_and_position_matters():
     a = o.forward([1, 2, 3], 0, [])
     b = o.forward([1, 2, 3], 5, [])        # shifted positions change the output (RoPE)
     assert not torch.allclose(a, b)
+
+
+def test_batched_decode_equals_per_sequence_forward():
+    o = _oracle()
+    prompts = [[5, 17, 250], [3, 99, 42, 7, 8], [11]]
+    kvs = []
+    for p in prompts:
+        kv: list = []
+        o.forward(p, 0, kv)
+        kvs.append(kv)
+    ref = []
+    for p in prompts:
+        kv: list = []
+        o.forward(p, 0, kv)
+        ref.append(o.forward([123], len(p), kv))
+    got = o.decode_batch([123] * 3, [len(p) for p in prompts], kvs)
+    assert torch.allclose(got, torch.stack(ref), atol=1e-5)
+    assert all(kv[0][0].shape[0] == len(p) + 1 for kv, p in zip(kvs, prompts))
