@@ -111,6 +111,9 @@ class EngineConfig:
     device: str = "auto"
     seed: int = 0
     skip_tokenizer_init: bool = False
+    # False: decode-only steps replay HIP graphs captured per padded batch size
+    enforce_eager: bool = False
+    max_graph_batch: int = 256
 
     def resolve(self) -> None:
         if self.device == "auto":

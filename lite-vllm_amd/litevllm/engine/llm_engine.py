@@ -8,13 +8,19 @@ step runs ONE forward for the whole scheduled batch (the reference runs one
 for the decodes plus one per prefill group, llm_engine.py:127-138) and
 samples every finished row with one lv_sample call and one device-to-host
 copy (the reference calls Sampler.sample and .item() per sequence,
-llm_engine.py:197).  Text is produced incrementally only when somebody reads
-it (streaming, or the final output).
+llm_engine.py:197).  Steps overlap: step k is launched before step k-1's
+sampled ids are read back, its decodes take their input ids straight from
+step k-1's device output, and the host bookkeeping of step k-1 runs while
+the GPU computes step k (a sequence that stops on EOS or a stop string thus
+computes one extra token, which is dropped; max_tokens is known ahead and
+costs nothing).  Text is produced incrementally only when somebody reads it
+(streaming, or the final output).
 """
 
 from __future__ import annotations
 
 import uuid
+from dataclasses import dataclass
 from typing import Optional
 
 import torch
@@ -29,6 +35,17 @@ from .scheduler import Scheduler
 from .sequence import Sequence, SequenceGroup, SequenceGroupOutput, SequenceStatus
 
 
+@dataclass
+class _InFlightStep:
+    """A launched step whose sampled ids have not been read back yet."""
+    groups: list[SequenceGroup]
+    sample_seqs: list[Sequence]
+    sample_groups: list[SequenceGroup]
+    ids_dev: Optional[torch.Tensor]     # sampled ids on the device
+    ids_host: Optional[torch.Tensor]    # their pinned host copy (async)
+    done: Optional["torch.cuda.Event"]  # recorded after the copy
+
+
 class LLMEngine:
     def __init__(self, engine_config: EngineConfig) -> None:
         self.config = engine_config
@@ -40,6 +57,7 @@ class LLMEngine:
         self.sampler = Sampler()
         self.stream_text = False   # AsyncLLM turns this on to get per-step deltas
         self._rng: Optional[torch.Generator] = None
+        self._inflight: Optional[_InFlightStep] = None
 
     def initialize(self) -> None:
         self.config.resolve()
@@ -52,11 +70,17 @@ class LLMEngine:
         if cc.num_gpu_blocks is None:
             cc.num_gpu_blocks = self.model_runner.profile_num_gpu_blocks()
         self.model_runner.init_kv_cache(cc.num_gpu_blocks)
-        self.block_manager = BlockManager(cc.block_size, cc.num_gpu_blocks, cc.num_cpu_blocks)
+        use_graphs = (not self.config.enforce_eager and self.config.device != "cpu"
+                      and torch.cuda.is_available())
+        # graph replays pad the batch with rows that write into block 0
+        self.block_manager = BlockManager(cc.block_size, cc.num_gpu_blocks, cc.num_cpu_blocks,
+                                          reserved_blocks=1 if use_graphs else 0)
         if cc.enable_prefix_caching:
             self.prefix_cache = PrefixCache(cc.block_size, self.block_manager)
         self.scheduler = Scheduler(self.config.scheduler_config, cc, self.block_manager,
                                    self.prefix_cache)
+        if use_graphs:
+            self.model_runner.capture_decode_graphs()
         dev = torch.device(self.config.device)
         self._rng = torch.Generator(device=dev)
         self._rng.manual_seed(self.config.seed)
@@ -79,41 +103,17 @@ class LLMEngine:
         return request_id
 
     def has_unfinished(self) -> bool:
-        return self.scheduler.has_unfinished()
+        return self.scheduler.has_unfinished() or self._inflight is not None
 
     def step(self) -> list[SequenceGroupOutput]:
+        """Launch this step's forward and sampling, then finish the previous
+        step (wait for its sampled ids, append them, apply the stop rules,
+        free finished sequences) while the GPU runs this one.  Returns the
+        outputs of the step that was finished."""
         sched = self.scheduler.schedule()
-        if sched.is_empty:
-            return []
-        meta = self.model_runner.prepare_inputs(sched.scheduled_seq_groups, self.block_manager)
-        # the forward runs even when no row is sampled: a chunk that does not
-        # finish its prompt still has to write its K/V
-        logits = self.model_runner.execute_model(meta)
-        tokens = self._sample(logits, meta) if meta.sample_seqs else []
-
-        sampled = {seq.seq_id: tok for seq, tok in zip(meta.sample_seqs, tokens)}
-        for sg in sched.scheduled_seq_groups:
-            for seq in sg.get_unfinished_seqs():
-                was_prefill = seq.is_prefill
-                if was_prefill:
-                    seq.num_computed_tokens += seq.num_scheduled_tokens or \
-                        (seq.data.prompt_len - seq.num_computed_tokens)
-                    if self.prefix_cache is not None:
-                        self.prefix_cache.insert(
-                            seq.data.prompt_token_ids[:seq.num_computed_tokens],
-                            self.block_manager.get_block_table(seq.seq_id))
-                else:
-                    seq.num_computed_tokens = seq.data.total_len
-                seq.num_scheduled_tokens = 0
-                tok = sampled.get(seq.seq_id)
-                if tok is not None:
-                    seq.data.append_token(tok)
-                    self._check_stop(seq, sg.sampling_params, tok)
-
-        outputs = [self._build_step_output(sg) for sg in sched.scheduled_seq_groups]
-        self.scheduler.update_running(sched.scheduled_seq_groups)
-        self.scheduler.free_finished()
-        return outputs
+        launched = None if sched.is_empty else self._launch(sched)
+        prev, self._inflight = self._inflight, launched
+        return self._finish(prev) if prev is not None else []
 
     def run_to_completion(self) -> list[SequenceGroupOutput]:
         finished: list[SequenceGroupOutput] = []
@@ -124,7 +124,61 @@ class LLMEngine:
         return finished
 
     # ------------------------------------------------------------------
-    def _sample(self, logits: torch.Tensor, meta) -> list[int]:
+    def _launch(self, sched) -> "_InFlightStep":
+        prev_ids = self._inflight.ids_dev if self._inflight is not None else None
+        meta = self.model_runner.prepare_inputs(sched.scheduled_seq_groups, self.block_manager,
+                                                device_tokens=prev_ids)
+        # the forward runs even when no row is sampled: a chunk that does not
+        # finish its prompt still has to write its K/V
+        logits = self.model_runner.execute_model(meta)
+        ids_dev = ids_host = done = None
+        if meta.sample_seqs:
+            ids_dev = self._sample(logits, meta)
+            ids_host = ids_dev.to("cpu", non_blocking=True)
+            done = torch.cuda.Event()
+            done.record()
+        # progress is booked at launch: later steps are ordered after this
+        # one on the stream, so they see its K/V
+        for sg in sched.scheduled_seq_groups:
+            for seq in sg.get_unfinished_seqs():
+                if seq.is_prefill:
+                    seq.num_computed_tokens += seq.num_scheduled_tokens or \
+                        (seq.data.prompt_len - seq.num_computed_tokens)
+                    if self.prefix_cache is not None:
+                        self.prefix_cache.insert(
+                            seq.data.prompt_token_ids[:seq.num_computed_tokens],
+                            self.block_manager.get_block_table(seq.seq_id))
+                else:
+                    seq.num_computed_tokens = seq.data.total_len + seq.num_inflight
+                seq.num_scheduled_tokens = 0
+        for row, seq in enumerate(meta.sample_seqs):
+            seq.num_inflight += 1
+            seq.inflight_row = row
+        return _InFlightStep(sched.scheduled_seq_groups, meta.sample_seqs, meta.sample_groups,
+                             ids_dev, ids_host, done)
+
+    def _finish(self, step: "_InFlightStep") -> list[SequenceGroupOutput]:
+        if step.ids_host is not None:
+            step.done.synchronize()
+            for seq, sg, tok in zip(step.sample_seqs, step.sample_groups, step.ids_host.tolist()):
+                seq.num_inflight -= 1
+                if seq.status.is_finished:      # stopped before this step's token arrived
+                    continue
+                seq.data.append_token(tok)
+                self._check_stop(seq, sg.sampling_params, tok)
+        outputs = []
+        for sg in step.groups:
+            if sg.final_output_sent:
+                continue
+            out = self._build_step_output(sg)
+            sg.final_output_sent = out.finished
+            outputs.append(out)
+        self.scheduler.update_running(step.groups)
+        self.scheduler.free_finished()
+        return outputs
+
+    def _sample(self, logits: torch.Tensor, meta) -> torch.Tensor:
+        """Sampled ids of meta.sample_seqs as a device tensor (no host sync)."""
         groups = meta.sample_groups
         simple = all(sg.sampling_params.top_k <= 0 and sg.sampling_params.top_p >= 1.0
                      for sg in groups)
@@ -133,10 +187,10 @@ class LLMEngine:
             temps = torch.tensor([sg.sampling_params.temperature for sg in groups],
                                  dtype=torch.float32).to(dev, non_blocking=True)
             uni = torch.rand(len(groups), dtype=torch.float32, device=dev, generator=self._rng)
-            return self.sampler.sample_batched(logits, temps, uni).tolist()
+            return self.sampler.sample_batched(logits, temps, uni)
         out = [self.sampler.sample(logits[i], sg.sampling_params, generator=self._rng)
                for i, sg in enumerate(groups)]
-        return torch.cat(out).tolist()
+        return torch.cat(out)
 
     def _check_stop(self, seq: Sequence, params: SamplingParams, token_id: int) -> None:
         eos = self.tokenizer.eos_token_id if self.tokenizer is not None else None

@@ -71,7 +71,7 @@ class InputMetadata:
                  sample_seqs: Optional[list[Sequence]] = None,
                  sample_groups: Optional[list[SequenceGroup]] = None,
                  num_decodes: int = 0, num_context_tokens: int = 0,
-                 num_context_blocks: int = 0) -> None:
+                 num_context_blocks: int = 0, graph_batch: Optional[int] = None) -> None:
         self.input_ids = input_ids
         self.positions = positions
         self.slot_mapping = slot_mapping
@@ -86,6 +86,7 @@ class InputMetadata:
         self.num_decodes = num_decodes                 # leading 1-token sequences
         self.num_context_tokens = num_context_tokens   # sum of context lengths (host)
         self.num_context_blocks = num_context_blocks   # sum of block-table lengths (host)
+        self.graph_batch = graph_batch                 # padded batch of a graph replay
 
 
 @dataclass
@@ -102,6 +103,8 @@ class StepDescriptors:
     max_blocks: int
     max_query_len: int
     is_prefill: bool
+    num_tokens: int = 0          # packed tokens (host-fed + device-fed)
+    uses_device_tokens: bool = False
 
 
 def build_step(seq_groups: list[SequenceGroup], block_manager) -> StepDescriptors:
@@ -110,7 +113,10 @@ def build_step(seq_groups: list[SequenceGroup], block_manager) -> StepDescriptor
     scheduler, the rest of the prompt as the reference does,
     model_runner.py:201-205) and samples when it reaches the prompt's end; a
     decode feeds its last token at position total_len - 1
-    (model_runner.py:217-229)."""
+    (model_runner.py:217-229).  When that last token is still in flight
+    (sampled by the previous step, not yet on the host) the descriptor
+    points at its row of the previous step's sampled ids (token_index) and
+    the position is total_len + num_inflight - 1."""
     seqs = [(sg, s) for sg in seq_groups for s in sg.get_unfinished_seqs()]
     B = len(seqs)
     descs = np.empty((B, 6), dtype=np.int32)
@@ -122,9 +128,11 @@ def build_step(seq_groups: list[SequenceGroup], block_manager) -> StepDescriptor
     seq_ids: list[int] = []
     n_blocks = n_tok = max_blocks = max_q = num_decodes = 0
     is_prefill = False
+    uses_device_tokens = False
     for i, (sg, seq) in enumerate(seqs):
         ids = block_manager.get_block_table(seq.seq_id).ids
         seq_ids.append(seq.seq_id)
+        tok_off, tok_index = len(tokens), -1
         if seq.is_prefill:
             is_prefill = True
             nc = seq.num_computed_tokens
@@ -134,11 +142,15 @@ def build_step(seq_groups: list[SequenceGroup], block_manager) -> StepDescriptor
         else:
             if i == num_decodes:
                 num_decodes += 1
-            nc = seq.data.total_len - 1
+            nc = seq.data.total_len + seq.num_inflight - 1
             q = 1
-            tokens.append(seq.data.last_token)
+            if seq.num_inflight > 0:
+                tok_index = seq.inflight_row
+                uses_device_tokens = True
+            else:
+                tokens.append(seq.data.last_token)
             samples = True
-        descs[i] = (nc, q, len(ids), n_blocks, n_tok, -1)
+        descs[i] = (nc, q, len(ids), n_blocks, tok_off, tok_index)
         tables.append(ids)
         n_blocks += len(ids)
         n_tok += q
@@ -150,19 +162,32 @@ def build_step(seq_groups: list[SequenceGroup], block_manager) -> StepDescriptor
             sample_groups.append(sg)
     block_ids = np.fromiter((b for t in tables for b in t), dtype=np.int32, count=n_blocks)
     return StepDescriptors(descs, block_ids, tokens, logits_rows, sample_seqs, sample_groups,
-                           seq_ids, num_decodes, max_blocks, max_q, is_prefill)
+                           seq_ids, num_decodes, max_blocks, max_q, is_prefill, n_tok,
+                           uses_device_tokens)
 
 
 class _Staging:
-    """Grow-only pinned host buffers for one step's packing inputs."""
+    """Grow-only pinned host buffers for one step's packing inputs.  The
+    copies out of them are asynchronous, so get() first waits for the
+    previous step's copies (record() marks them) before the host rewrites
+    the buffers."""
 
     def __init__(self) -> None:
+        self._event: Optional[torch.cuda.Event] = None
         self.i32 = torch.empty(0, dtype=torch.int32).pin_memory() if torch.cuda.is_available() \
             else torch.empty(0, dtype=torch.int32)
         self.i64 = torch.empty(0, dtype=torch.int64).pin_memory() if torch.cuda.is_available() \
             else torch.empty(0, dtype=torch.int64)
 
+    def record(self) -> None:
+        if torch.cuda.is_available():
+            if self._event is None:
+                self._event = torch.cuda.Event()
+            self._event.record()
+
     def get(self, n32: int, n64: int) -> tuple[torch.Tensor, torch.Tensor]:
+        if self._event is not None:
+            self._event.synchronize()
         if self.i32.numel() < n32:
             self.i32 = torch.empty(max(n32, 2 * self.i32.numel()), dtype=torch.int32,
                                    pin_memory=torch.cuda.is_available())
@@ -170,6 +195,140 @@ class _Staging:
             self.i64 = torch.empty(max(n64, 2 * self.i64.numel()), dtype=torch.int64,
                                    pin_memory=torch.cuda.is_available())
         return self.i32[:n32], self.i64[:n64]
+
+
+GRAPH_BATCHES = (1, 2, 4, 8, 16, 24, 32, 48, 64, 80, 96, 112, 128, 144, 160, 176, 192, 208,
+                 224, 240, 256, 320, 384, 448, 512)
+
+
+class DecodeGraphs:
+    """HIP graphs of the decode-only forward, one per padded batch size.
+
+    All graphs read one set of static buffers: the packing kernel runs
+    eagerly before a replay and writes input ids, positions, slots, context
+    lengths and block tables (max_blocks = max_model_len / block_size wide)
+    into them.  A batch of B decodes replays the graph of the smallest
+    captured size b >= B; the b - B padding rows are one-token sequences
+    without blocks, so their slot is 0 -- block 0 is reserved as scratch
+    (the reference's convention, cache/block_manager.py:20-27) -- and their
+    logits are dropped.  The attention workspace is sized for the largest
+    batch and owned here, so no replay reads memory another call may free.
+    """
+
+    def __init__(self, runner: "ModelRunner", max_batch: int) -> None:
+        mc = runner.model_config
+        cc = runner.config.cache_config
+        dev = torch.device(runner.device)
+        self.runner = runner
+        self.block_size = cc.block_size
+        self.max_blocks = (mc.max_model_len + cc.block_size - 1) // cc.block_size
+        self.batches = [b for b in GRAPH_BATCHES if b < max_batch] + [max_batch]
+        n = max_batch
+        self.descs = torch.zeros((n, 6), dtype=torch.int32, device=dev)
+        self.block_ids = torch.zeros(n * self.max_blocks, dtype=torch.int32, device=dev)
+        self.token_ids = torch.zeros(n, dtype=torch.int64, device=dev)
+        self.packed = {
+            "input_ids": torch.zeros(n, dtype=torch.int64, device=dev),
+            "positions": torch.zeros(n, dtype=torch.int64, device=dev),
+            "slot_mapping": torch.zeros(n, dtype=torch.int64, device=dev),
+            "cu_seqlens": torch.zeros(n + 1, dtype=torch.int32, device=dev),
+            "seq_start": torch.zeros(n, dtype=torch.int32, device=dev),
+            "context_lens": torch.zeros(n, dtype=torch.int32, device=dev),
+            "block_tables": torch.zeros((n, self.max_blocks), dtype=torch.int32, device=dev),
+        }
+        ws = max(ops.paged_attention_workspace_size(b, b, b, mc.num_attention_heads, mc.head_dim,
+                                                    cc.block_size, self.max_blocks, 1,
+                                                    mc.torch_dtype) for b in self.batches)
+        self.workspace = torch.empty(max(ws, 256), dtype=torch.uint8, device=dev)
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.logits: dict[int, torch.Tensor] = {}
+        tmpl = torch.zeros((n, 6), dtype=torch.int32)
+        tmpl[:, 1] = 1                                   # query_len 1
+        tmpl[:, 4] = torch.arange(n, dtype=torch.int32)  # token_offset = row
+        tmpl[:, 5] = -1                                  # ids from token_ids
+        self._pad_template = tmpl.to(dev)
+
+    def _views(self, b: int) -> dict[str, torch.Tensor]:
+        p = self.packed
+        return {"input_ids": p["input_ids"][:b], "positions": p["positions"][:b],
+                "slot_mapping": p["slot_mapping"][:b], "cu_seqlens": p["cu_seqlens"][:b + 1],
+                "seq_start": p["seq_start"][:b], "context_lens": p["context_lens"][:b],
+                "block_tables": p["block_tables"][:b]}
+
+    def _forward(self, b: int) -> torch.Tensor:
+        v = self._views(b)
+        meta = AttentionMetadata(block_tables=v["block_tables"], context_lens=v["context_lens"],
+                                 cu_seqlens=v["cu_seqlens"], num_decodes=b, max_query_len=1,
+                                 workspace=self.workspace)
+        r = self.runner
+        kv = [r.kv_cache.get_kv(i) for i in range(r.model_config.num_hidden_layers)]
+        return r.model(input_ids=v["input_ids"], positions=v["positions"], kv_caches=kv,
+                       slot_mapping=v["slot_mapping"], block_tables=v["block_tables"],
+                       context_lens=v["context_lens"], is_prefill=False, attn_metadata=meta,
+                       logits_indices=None)
+
+    def _pack(self, b: int, num_block_ids: int,
+              device_tokens: Optional[torch.Tensor] = None) -> None:
+        ops.pack_inputs(self.descs[:b], self.block_ids[:max(num_block_ids, 1)],
+                        self.token_ids[:b], b, self.block_size, self.max_blocks,
+                        device_tokens=device_tokens, out=self._views(b))
+
+    @torch.inference_mode()
+    def capture(self) -> None:
+        pool = torch.cuda.graph_pool_handle()
+        for b in sorted(self.batches, reverse=True):
+            self._pad_rows(0, b)
+            self._pack(b, 1)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                self._forward(b)
+            torch.cuda.current_stream().wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=pool):
+                self.logits[b] = self._forward(b)
+            self.graphs[b] = g
+        torch.cuda.synchronize()
+
+    def accepts(self, st: StepDescriptors) -> bool:
+        B = st.descs.shape[0]
+        return (B > 0 and st.num_decodes == B and B <= self.batches[-1]
+                and st.max_blocks <= self.max_blocks and bool(self.graphs))
+
+    def prepare(self, st: StepDescriptors, staging: "_Staging",
+                device_tokens: Optional[torch.Tensor]) -> InputMetadata:
+        B = st.descs.shape[0]
+        b = next(x for x in self.batches if x >= B)
+        nb = st.block_ids.shape[0]
+        n_host = len(st.tokens)
+        st32, st64 = staging.get(B * 6 + nb, max(n_host, 1))
+        a32 = st32.numpy()
+        a32[:B * 6] = st.descs.reshape(-1)
+        a32[B * 6:] = st.block_ids
+        st64.numpy()[:n_host] = st.tokens
+        self.descs[:B].view(-1).copy_(st32[:B * 6], non_blocking=True)
+        self.block_ids[:nb].copy_(st32[B * 6:], non_blocking=True)
+        if n_host:
+            self.token_ids[:n_host].copy_(st64[:n_host], non_blocking=True)
+        staging.record()
+        if b > B:
+            self._pad_rows(B, b)
+        self._pack(b, nb, device_tokens)
+        return InputMetadata(None, None, None, None, None, False, st.seq_ids,
+                             sample_seqs=st.sample_seqs, sample_groups=st.sample_groups,
+                             num_decodes=B,
+                             num_context_tokens=int(st.descs[:, 0].sum() + st.descs[:, 1].sum()),
+                             num_context_blocks=int(nb), graph_batch=b)
+
+    def _pad_rows(self, start: int, b: int) -> None:
+        """Descriptors start..b-1 become padding: one token (id 0) at
+        position 0 with no blocks, i.e. slot 0 in the scratch block."""
+        self.descs[start:b].copy_(self._pad_template[start:b])
+        self.token_ids[start:b].zero_()
+
+    def replay(self, meta: InputMetadata) -> torch.Tensor:
+        self.graphs[meta.graph_batch].replay()
+        return self.logits[meta.graph_batch][:meta.num_decodes]
 
 
 class ModelRunner:
@@ -180,6 +339,7 @@ class ModelRunner:
         self.model: Optional[BaseModelForCausalLM] = None
         self.kv_cache: Optional[KVCache] = None
         self._staging = _Staging()
+        self.graphs: Optional[DecodeGraphs] = None
 
     def load_model(self) -> None:
         mc = self.model_config
@@ -216,31 +376,50 @@ class ModelRunner:
                                        mc.num_key_value_heads, mc.head_dim, mc.torch_dtype)
         return max(n, 16)
 
+    def capture_decode_graphs(self) -> None:
+        """Capture the decode-only forward for every padded batch size up to
+        the scheduler's max_num_seqs (block 0 must be reserved as scratch)."""
+        max_batch = min(self.config.max_graph_batch, self.config.scheduler_config.max_num_seqs)
+        graphs = DecodeGraphs(self, max_batch)
+        graphs.capture()
+        self.graphs = graphs
+
     # ------------------------------------------------------------------
-    def prepare_inputs(self, seq_groups: list[SequenceGroup], block_manager) -> InputMetadata:
-        """Pack the scheduled sequences (decodes first, then prefill chunks)."""
+    def prepare_inputs(self, seq_groups: list[SequenceGroup], block_manager,
+                       device_tokens: Optional[torch.Tensor] = None) -> InputMetadata:
+        """Pack the scheduled sequences (decodes first, then prefill chunks).
+        ``device_tokens``: the previous step's sampled ids, read by decodes
+        whose last token is still in flight."""
         st = build_step(seq_groups, block_manager)
-        B, n_blocks, n_tok = st.descs.shape[0], st.block_ids.shape[0], len(st.tokens)
+        if st.uses_device_tokens and device_tokens is None:
+            raise RuntimeError("a decode's last token is in flight but no device tokens were given")
+        if self.graphs is not None and self.graphs.accepts(st):
+            return self.graphs.prepare(st, self._staging, device_tokens)
+        B, n_blocks = st.descs.shape[0], st.block_ids.shape[0]
+        n_host, T = len(st.tokens), st.num_tokens
+        h = max(n_host, 1)                   # keep the id array non-empty
         dev = torch.device(self.device)
         n32 = B * 6 + n_blocks
-        st32, st64 = self._staging.get(n32, n_tok + len(st.logits_rows))
+        st32, st64 = self._staging.get(n32, h + len(st.logits_rows))
         a32 = st32.numpy()
         a32[:B * 6] = st.descs.reshape(-1)
         a32[B * 6:n32] = st.block_ids
         a64 = st64.numpy()
-        a64[:n_tok] = st.tokens
-        a64[n_tok:] = st.logits_rows
+        a64[:n_host] = st.tokens
+        a64[h:] = st.logits_rows
         d32 = st32.to(dev, non_blocking=True)
         d64 = st64.to(dev, non_blocking=True)
-        packed = ops.pack_inputs(d32[:B * 6].view(B, 6), d32[B * 6:], d64[:n_tok], n_tok,
-                                 self.config.cache_config.block_size, max(st.max_blocks, 1))
+        self._staging.record()
+        packed = ops.pack_inputs(d32[:B * 6].view(B, 6), d32[B * 6:], d64[:h], T,
+                                 self.config.cache_config.block_size, max(st.max_blocks, 1),
+                                 device_tokens=device_tokens)
         attn = AttentionMetadata(block_tables=packed["block_tables"],
                                  context_lens=packed["context_lens"],
                                  cu_seqlens=packed["cu_seqlens"], num_decodes=st.num_decodes,
                                  max_query_len=st.max_query_len)
         return InputMetadata(packed["input_ids"], packed["positions"], packed["slot_mapping"],
                              packed["block_tables"], packed["context_lens"], st.is_prefill,
-                             st.seq_ids, attn_metadata=attn, logits_indices=d64[n_tok:],
+                             st.seq_ids, attn_metadata=attn, logits_indices=d64[h:],
                              sample_seqs=st.sample_seqs, sample_groups=st.sample_groups,
                              num_decodes=st.num_decodes,
                              num_context_tokens=int(st.descs[:, 0].sum() + st.descs[:, 1].sum()),
@@ -249,6 +428,8 @@ class ModelRunner:
     @torch.inference_mode()
     def execute_model(self, metadata: InputMetadata) -> torch.Tensor:
         """Forward pass; logits of the sampled rows only ([len(sample_seqs), V])."""
+        if metadata.graph_batch is not None:
+            return self.graphs.replay(metadata)
         kv_caches = None
         if self.kv_cache is not None:
             kv_caches = [self.kv_cache.get_kv(i) for i in range(self.model_config.num_hidden_layers)]

@@ -106,12 +106,20 @@ class Scheduler:
                 if used_seqs + len(seqs) > budget_seqs or used_tokens >= budget_tokens:
                     continue
                 if phase == "decode":
-                    need = sum(self._blocks_missing(s.seq_id, s.data.total_len) for s in seqs)
+                    # a token still in flight counts: the next position is
+                    # total_len + num_inflight - 1; a sequence whose in-flight
+                    # tokens already reach max_tokens is finishing, not fed
+                    max_tokens = sg.sampling_params.max_tokens
+                    if all(s.data.output_len + s.num_inflight >= max_tokens for s in seqs):
+                        continue
+                    need = sum(self._blocks_missing(s.seq_id, s.data.total_len + s.num_inflight)
+                               for s in seqs)
                     if used_tokens + len(seqs) > budget_tokens or \
                             (need > 0 and not self.block_manager.can_allocate(need)):
                         continue
                     for s in seqs:
-                        self._grow(s.seq_id, self._blocks_missing(s.seq_id, s.data.total_len))
+                        self._grow(s.seq_id, self._blocks_missing(
+                            s.seq_id, s.data.total_len + s.num_inflight))
                         s.num_scheduled_tokens = 1
                     used_tokens += len(seqs)
                     decodes.append(sg)

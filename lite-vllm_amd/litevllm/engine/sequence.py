@@ -2,7 +2,10 @@
 SequenceGroupOutput with the reference's fields and meanings
 (engine/sequence.py:17-167).  Additions for real chunked prefill and cheap
 per-step packing: ``Sequence.num_scheduled_tokens`` (tokens fed this step)
-and ``SequenceData.last_token`` (no prompt+output list concatenation)."""
+and ``SequenceData.last_token`` (no prompt+output list concatenation); for
+the overlapped step loop, ``Sequence.num_inflight`` / ``inflight_row``: a
+token sampled on the device by the step in flight, not yet appended on the
+host, and its row in that step's sampled-ids tensor."""
 
 from __future__ import annotations
 
@@ -72,6 +75,8 @@ class Sequence:
     num_computed_tokens: int = 0   # tokens whose KV is in the cache
     emitted_text: str = ""
     num_scheduled_tokens: int = 0  # tokens fed in the current step
+    num_inflight: int = 0          # sampled on the device, not yet appended here
+    inflight_row: int = -1         # row of the newest such token in its step's ids
 
     @classmethod
     def create(cls, prompt_token_ids: list[int]) -> "Sequence":
@@ -99,6 +104,7 @@ class SequenceGroup:
     sampling_params: SamplingParams
     arrival_time: float = field(default_factory=time.time)
     prompt_text: str = ""
+    final_output_sent: bool = False   # the finished output was returned once
 
     @classmethod
     def create(cls, request_id: str, prompt_token_ids: list[int], sampling_params: SamplingParams,

@@ -24,7 +24,7 @@ class LLM:
                  chunk_size: int = 512, trust_remote_code: bool = True, seed: int = 0,
                  load_format: str = "auto", hf_overrides: Optional[dict] = None,
                  skip_tokenizer_init: bool = False, num_gpu_blocks: Optional[int] = None,
-                 device: str = "auto") -> None:
+                 device: str = "auto", enforce_eager: bool = False) -> None:
         cfg = EngineConfig(
             model_config=ModelConfig(model=model, dtype=dtype, max_model_len=max_model_len,
                                      trust_remote_code=trust_remote_code,
@@ -36,7 +36,8 @@ class LLM:
                                              max_num_batched_tokens=max_num_batched_tokens,
                                              chunked_prefill=chunked_prefill,
                                              chunk_size=chunk_size),
-            device=device, seed=seed, skip_tokenizer_init=skip_tokenizer_init)
+            device=device, seed=seed, skip_tokenizer_init=skip_tokenizer_init,
+            enforce_eager=enforce_eager)
         self.engine = LLMEngine(cfg)
         self.engine.initialize()
 

@@ -31,6 +31,7 @@ class AttentionMetadata:
     cu_seqlens: torch.Tensor     # int32 [B+1]
     num_decodes: int             # leading 1-token sequences
     max_query_len: int
+    workspace: Optional[torch.Tensor] = None   # attention scratch owned by a HIP graph
 
 
 class PagedAttention:
@@ -59,7 +60,8 @@ class Attention(nn.Module):
             m = attn_metadata
             return ops.paged_attention(query, key_cache, value_cache, m.block_tables,
                                        m.context_lens, scale=self.scale, cu_seqlens=m.cu_seqlens,
-                                       num_decodes=m.num_decodes, max_query_len=m.max_query_len)
+                                       num_decodes=m.num_decodes, max_query_len=m.max_query_len,
+                                       workspace=m.workspace)
         if is_prefill:
             return self._prefill(query, key, value)
         return ops.paged_attention(query, key_cache, value_cache, block_table, context_lens,

@@ -122,7 +122,8 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
                     num_kv_heads: Optional[int] = None, scale: float,
                     cu_seqlens: Optional[torch.Tensor] = None,
                     num_decodes: Optional[int] = None, max_query_len: int = 1,
-                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    out: Optional[torch.Tensor] = None,
+                    workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Attention of every query row over its sequence's paged K/V.
 
     Reference: litevllm/layers/attention.py:91-139 (decode) and 141-151
@@ -130,6 +131,9 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
     block_tables int32 [B, max_blocks]; context_lens int32 [B] (tokens in
     cache incl. this step's); cu_seqlens int32 [B+1] (None => T == B, all
     decodes); the first ``num_decodes`` sequences must be 1-token decodes.
+    ``workspace`` (uint8, at least paged_attention_workspace_size bytes) is
+    used instead of the per-stream scratch buffer when given: a captured HIP
+    graph must own the memory its kernels read.
     """
     dev = key_cache.device
     for n, t in (("query", query), ("key_cache", key_cache), ("value_cache", value_cache),
@@ -174,7 +178,14 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
     dt = _dtype_code(query)
     ws_bytes = lib.lv_paged_attention_workspace_size(B, num_decodes, T, H, D, bs, max_blocks,
                                                      max_query_len, dt)
-    ws = _workspace(dev, ws_bytes)
+    if workspace is not None:
+        _require_device("workspace", workspace, dev)
+        if workspace.dtype != torch.uint8 or not workspace.is_contiguous() or \
+                workspace.numel() < ws_bytes:
+            raise RuntimeError(f"workspace must be a contiguous uint8 tensor of >= {ws_bytes} bytes")
+        ws = workspace if ws_bytes > 0 else None
+    else:
+        ws = _workspace(dev, ws_bytes)
     rc = lib.lv_paged_attention(
         _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache), n_blocks,
         _ptr(block_tables), max_blocks, _ptr(cu_seqlens), _ptr(context_lens),
@@ -184,13 +195,25 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
     return out
 
 
+def paged_attention_workspace_size(num_seqs: int, num_decodes: int, num_tokens: int,
+                                   num_heads: int, head_dim: int, block_size: int,
+                                   max_blocks: int, max_query_len: int,
+                                   dtype: torch.dtype) -> int:
+    """Bytes of scratch one lv_paged_attention call with these sizes needs."""
+    lib = _hip.load()
+    return int(lib.lv_paged_attention_workspace_size(num_seqs, num_decodes, num_tokens,
+                                                     num_heads, head_dim, block_size, max_blocks,
+                                                     max_query_len, _DTYPE_CODES[dtype]))
+
+
 # ---------------------------------------------------------------------------
 # (1) packing
 # ---------------------------------------------------------------------------
 
 def pack_inputs(descs: torch.Tensor, block_ids: torch.Tensor, token_ids: torch.Tensor,
                 num_tokens: int, block_size: int, max_blocks: int,
-                device_tokens: Optional[torch.Tensor] = None) -> dict[str, torch.Tensor]:
+                device_tokens: Optional[torch.Tensor] = None,
+                out: Optional[dict[str, torch.Tensor]] = None) -> dict[str, torch.Tensor]:
     """Expand per-sequence descriptors into the packed step tensors on the GPU.
 
     Reference: ModelRunner.prepare_inputs, litevllm/engine/model_runner.py:180-260.
@@ -199,7 +222,8 @@ def pack_inputs(descs: torch.Tensor, block_ids: torch.Tensor, token_ids: torch.T
     device_tokens int64 [*] or None.
     Returns input_ids/positions/slot_mapping (int64 [T]), cu_seqlens
     (int32 [B+1]), seq_start/context_lens (int32 [B]) and block_tables
-    (int32 [B, max_blocks]).
+    (int32 [B, max_blocks]); with ``out`` given (same keys, exactly those
+    shapes, contiguous) they are written in place.
     """
     dev = descs.device
     for n, t in (("descs", descs), ("block_ids", block_ids), ("token_ids", token_ids),
@@ -214,15 +238,18 @@ def pack_inputs(descs: torch.Tensor, block_ids: torch.Tensor, token_ids: torch.T
         _check_int("device_tokens", device_tokens, torch.int64, 1)
     B = descs.shape[0]
     T = int(num_tokens)
-    out = {
-        "input_ids": torch.empty(T, dtype=torch.int64, device=dev),
-        "positions": torch.empty(T, dtype=torch.int64, device=dev),
-        "slot_mapping": torch.empty(T, dtype=torch.int64, device=dev),
-        "cu_seqlens": torch.empty(B + 1, dtype=torch.int32, device=dev),
-        "seq_start": torch.empty(B, dtype=torch.int32, device=dev),
-        "context_lens": torch.empty(B, dtype=torch.int32, device=dev),
-        "block_tables": torch.empty((B, max_blocks), dtype=torch.int32, device=dev),
-    }
+    shapes = {"input_ids": ((T,), torch.int64), "positions": ((T,), torch.int64),
+              "slot_mapping": ((T,), torch.int64), "cu_seqlens": ((B + 1,), torch.int32),
+              "seq_start": ((B,), torch.int32), "context_lens": ((B,), torch.int32),
+              "block_tables": ((B, max_blocks), torch.int32)}
+    if out is None:
+        out = {k: torch.empty(shp, dtype=dt, device=dev) for k, (shp, dt) in shapes.items()}
+    else:
+        for k, (shp, dt) in shapes.items():
+            t = out[k]
+            _require_device(k, t, dev)
+            if tuple(t.shape) != shp or t.dtype != dt or not t.is_contiguous():
+                raise RuntimeError(f"out[{k!r}] must be a contiguous {dt} tensor of shape {shp}")
     lib = _hip.load()
     rc = lib.lv_pack_inputs(
         _ptr(descs), B, _ptr(block_ids), block_ids.numel(), _ptr(token_ids), token_ids.numel(),

@@ -237,7 +237,7 @@ def test_engine_runs_forward_for_chunks_that_sample_nothing():
     class StubRunner:
         calls = 0
 
-        def prepare_inputs(self, groups, bm):
+        def prepare_inputs(self, groups, bm, device_tokens=None):
             st = build_step(groups, bm)
             return type("M", (), {"sample_seqs": st.sample_seqs, "sample_groups": st.sample_groups})
 
@@ -254,3 +254,51 @@ def test_engine_runs_forward_for_chunks_that_sample_nothing():
     assert StubRunner.calls == 1 and sg.seqs[0].num_computed_tokens == 64
     eng.step()
     assert StubRunner.calls == 2 and sg.seqs[0].num_computed_tokens == 128
+
+
+def test_build_step_feeds_inflight_tokens_from_the_device():
+    """A decode whose last token is still in flight reads it from the
+    previous step's sampled ids (token_index = its row) at position
+    total_len + num_inflight - 1; the result equals the literal packing of
+    the same sequence with that token appended on the host."""
+    bs = 16
+    bm = BlockManager(bs, 64)
+    groups, recs = [], []
+    prev_ids = np.array([900, 901, 902, 903], dtype=np.int64)
+    for i, (plen, n_out, row) in enumerate([(20, 3, 2), (33, 0, 0), (5, 7, -1)]):
+        sg = SequenceGroup.create(f"r{i}", list(range(100 * i, 100 * i + plen)), SamplingParams())
+        seq = sg.seqs[0]
+        seq.num_computed_tokens = plen
+        for t in range(n_out):
+            seq.data.append_token(50 + t)
+        if row >= 0:
+            seq.num_inflight, seq.inflight_row = 1, row
+        bm.allocate(seq.seq_id, (seq.data.total_len + seq.num_inflight + bs - 1) // bs)
+        groups.append(sg)
+        out = seq.data.output_token_ids + ([int(prev_ids[row])] if row >= 0 else [])
+        recs.append(SeqRecord(seq.data.prompt_token_ids, out, plen,
+                              bm.get_block_table(seq.seq_id).ids))
+    st = build_step(groups, bm)
+    assert st.uses_device_tokens and st.num_tokens == 3 and len(st.tokens) == 1
+    assert st.descs[:, 5].tolist() == [2, 0, -1]
+    got = expand_descriptors(st.descs, st.block_ids, np.asarray(st.tokens, np.int64), bs,
+                             st.max_blocks, device_tokens=prev_ids)
+    lit = prepare_inputs_literal(recs, bs)
+    for k in ("input_ids", "positions", "slot_mapping"):
+        assert got[k].tolist() == lit[k], k
+    assert got["context_lens"].tolist() == lit["context_lens"]
+
+
+def test_scheduler_counts_inflight_tokens_and_skips_finishing_sequences():
+    s = _sched(bs=4, blocks=16)
+    sg = _req(s, "a", 4, max_tokens=3)
+    out = s.schedule()
+    _advance(s, out)                       # prompt done, 1 output token on the host
+    seq = sg.seqs[0]
+    seq.num_inflight, seq.inflight_row = 1, 0
+    out = s.schedule()                     # position total_len + 1 - 1 = 5 -> 2 blocks
+    assert out.num_decode_groups == 1
+    assert len(s.block_manager.get_block_table(seq.seq_id)) == 2
+    seq.num_scheduled_tokens = 0
+    seq.num_inflight = 2                   # 1 on host + 2 in flight reach max_tokens=3
+    assert s.schedule().is_empty

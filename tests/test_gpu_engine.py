@@ -79,16 +79,20 @@ def test_attention_reference_signature_paths(device):
     assert torch.equal(kc[0, :2].cpu(), k[:2])
 
 
-def test_config1_tiny_llama_matches_cpu_oracle(device):
+@pytest.mark.parametrize("eager", [True, False])
+def test_config1_tiny_llama_matches_cpu_oracle(device, eager):
     """Config 1: 8 prompts (lengths U[16,64], ids U[0,32000)), greedy, 32
     tokens, ignore EOS, bs 16, chunk 512, fp32.  Every token equals the CPU
-    oracle's until the oracle's top-2 logit margin falls below 1e-4."""
-    _say("config1 tiny llama")
+    oracle's until the oracle's top-2 logit margin falls below 1e-4; with
+    and without the decode HIP graphs."""
+    _say(f"config1 tiny llama eager={eager}")
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(16, 65, (8,), generator=g).tolist()
     prompts = [torch.randint(0, 32000, (n,), generator=g).tolist() for n in lens]
     llm = LLM("tiny-llama", dtype="float32", load_format="dummy", hf_overrides=TINY_LLAMA,
-              skip_tokenizer_init=True, num_gpu_blocks=256, block_size=16, chunk_size=512)
+              skip_tokenizer_init=True, num_gpu_blocks=256, block_size=16, chunk_size=512,
+              enforce_eager=eager)
+    assert (llm.engine.model_runner.graphs is None) == eager
     outs = llm.generate(prompt_token_ids=prompts,
                         sampling_params=SamplingParams(temperature=0.0, max_tokens=32,
                                                        ignore_eos=True))
@@ -190,3 +194,38 @@ def test_async_llm_streams_and_finishes(device):
 
     eng, chunks = asyncio.run(run())
     assert chunks == [] and not eng.has_unfinished   # no tokenizer: no text deltas
+
+
+def test_decode_graph_replays_match_eager_forward(device):
+    """Every replay of a captured decode graph equals the eager forward of
+    the same padded batch, with the engine's own eager work (prefill chunks,
+    sampling, host syncs) between the replays."""
+    _say("decode graph replays vs eager")
+    llm = LLM("tiny-qwen3", dtype="bfloat16", load_format="dummy", hf_overrides=QWEN3_SMALL,
+              skip_tokenizer_init=True, num_gpu_blocks=256, chunk_size=64)
+    eng = llm.engine
+    runner = eng.model_runner
+    assert runner.graphs is not None and eng.block_manager.gpu_allocator.reserved_blocks == 1
+    orig = runner.execute_model
+    seen = []
+
+    def checked(meta):
+        logits = orig(meta)
+        if meta.graph_batch is not None:
+            b = meta.graph_batch
+            replayed = runner.graphs.logits[b].clone()
+            with torch.inference_mode():
+                eager = runner.graphs._forward(b)
+            torch.cuda.synchronize()
+            assert torch.equal(replayed, eager), f"replay {len(seen)}: batch {meta.num_decodes} -> {b}"
+            seen.append((meta.num_decodes, b))
+        return logits
+
+    runner.execute_model = checked
+    g = torch.Generator().manual_seed(5)
+    prompts = [torch.randint(0, 5000, (40 + 13 * i,), generator=g).tolist() for i in range(5)]
+    outs = llm.generate(prompt_token_ids=prompts,
+                        sampling_params=SamplingParams(temperature=0.0, max_tokens=12,
+                                                       ignore_eos=True))
+    assert all(o.num_output_tokens == 12 for o in outs)
+    assert len(seen) >= 5 and any(B < b for B, b in seen)   # padded replays included
