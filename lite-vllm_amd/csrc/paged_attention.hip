@@ -517,75 +517,100 @@ __global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Prefill-chunk attention on MFMA (bf16 / fp16).
+// Prefill-chunk attention on MFMA (bf16 / fp16), v_mfma_f32_32x32x16.
 //
-// One workgroup (4 wavefronts) per (chunk sequence, kv head, tile of 64/G
-// query tokens): its 64 rows are (query token, GQA head) pairs that share one
-// kv head, wavefront w owning rows 16w..16w+15 (row r -> token r % QT,
-// group head r / QT).  Keys stream through LDS in tiles of 32 (two 16-token
-// blocks): K row-major, V transposed.  Per tile and wavefront:
-//   S^T = K Q^T   with v_mfma_f32_16x16x32 (A = K rows from LDS, B = the
-//                 wavefront's Q rows held in registers for the whole kernel);
-//                 lane l then holds query l % 16 against keys 4(l/16)+r and
-//                 16+4(l/16)+r (r = 0..3);
-//   causal mask (key <= query position), online softmax in fp32 (the four
-//   lanes of a query combine their max with two shuffles);
-//   O += P V      with the same instruction: the lane's eight probabilities,
-//                 converted to bf16/fp16, are exactly its A-operand slots once
-//                 the 32-key contraction index is permuted as
-//                 k = 8(l/16) + j -> key (j < 4 ? 4(l/16)+j : 16+4(l/16)+j-4);
-//                 the B operand reads V^T[dim][those keys] as two 8-byte LDS
-//                 loads.
-// K/V for the next tile (and the block ids two tiles ahead) are loaded into
-// registers while the current tile is computed.  Keys at or past the end of
-// the needed range are zero-filled, so they contribute exactly nothing.
+// One workgroup (4 wavefronts) per (chunk sequence, kv head, tile of 128/G
+// query tokens).  Its 128 rows are (query token, GQA head) pairs sharing the
+// kv head: row r -> token r % QT, group head r / QT; wavefront w owns rows
+// 32w..32w+31 and holds their Q for the whole kernel.  Keys stream through
+// LDS in tiles of 64 (four 16-token blocks), double buffered: the next
+// tile's K/V are loaded from HBM into registers while the current tile is
+// computed, then written to the other buffer; one barrier per tile.  K and V
+// both stay in their natural [key][dim] layout in LDS (16-byte writes).
+// Per tile and wavefront:
+//   S^T = K Q^T      A = 32 key rows of K (16-byte LDS reads), B = Q^T from
+//                    registers; lane l ends with query l % 32 against keys
+//                    8(s/4) + 4(l/32) + s%4 of each 32-key half (s = slot);
+//   causal mask (key <= query position) and online softmax in fp32 -- the
+//   lane owns its query column, so max/sum need one shuffle (xor 32);
+//   O^T += V^T P^T   A = V^T read with ds_read_b64_tr_b16 (the LDS transpose
+//                    load: in each 16-lane group, lane j receives element
+//                    j % 4 of the 4-element reads of lanes 4s + j / 4, so
+//                    lanes reading 4 key rows x 16 dims get 4 keys of one dim
+//                    each), B = the lane's own probabilities in bf16/fp16
+//                    once the 16-key contraction index is permuted as
+//                    k = 8h + m -> key 4h + m % 4 + 8 (m / 4) (+16 per step).
+// O^T keeps the query as the column, so the softmax rescale is lane-local.
+// Keys at or past the end of the needed range are zero-filled and masked.
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x8_t __attribute__((ext_vector_type(8)));
 
-template <typename T> struct Mfma;
-template <> struct Mfma<bf16> {
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+template <typename T> struct Mfma32;
+template <> struct Mfma32<bf16> {
   using v8 = bf16x8_t;
-  __device__ __forceinline__ static f32x4_t run(v8 a, v8 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  __device__ __forceinline__ static f32x16_t run(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  __device__ __forceinline__ static v8 from_bits(const uint4& u) { return __builtin_bit_cast(v8, u); }
-  __device__ __forceinline__ static uint16_t to_bits(float f) { return float_to_bf16_bits(f); }
+  // Two fp32 values -> packed pair, round to nearest even (v_cvt_pk_bf16_f32).
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+  }
 };
-template <> struct Mfma<f16> {
+template <> struct Mfma32<f16> {
   using v8 = f16x8_t;
-  __device__ __forceinline__ static f32x4_t run(v8 a, v8 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  __device__ __forceinline__ static f32x16_t run(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  __device__ __forceinline__ static v8 from_bits(const uint4& u) { return __builtin_bit_cast(v8, u); }
-  __device__ __forceinline__ static uint16_t to_bits(float f) { return float_to_f16_bits(f); }
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
+    return (uint32_t)float_to_f16_bits(a) | ((uint32_t)float_to_f16_bits(b) << 16);
+  }
 };
 
 constexpr int kChunkThreads = 256;
-constexpr int kChunkKeys = 32;
+constexpr int kChunkRows = 128;   // (query token, head) rows per workgroup
+constexpr int kChunkKeys = 64;    // keys per LDS tile
+constexpr int kChunkVRow = 160;   // V row stride in LDS (elements): 80 dwords = 16 mod 64 banks
+
+template <int D> struct ChunkLds {
+  static constexpr int KROW = D + 8;  // 16-byte pad: 16 consecutive rows hit 16 distinct bank quads
+  static constexpr int VROW = kChunkVRow;
+  static constexpr int KBUF = kChunkKeys * KROW, VBUF = kChunkKeys * VROW;
+  static constexpr size_t BYTES = 2 * (size_t)(KBUF + VBUF) * sizeof(uint16_t);
+};
+
+__device__ __forceinline__ i16x4_t lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)p);
+}
 
 template <typename T, int D, int G, int BS>
-__global__ __launch_bounds__(kChunkThreads) void attn_chunk_mfma_kernel(
+__global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
     const T* __restrict__ q, int64_t q_stride,
     const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
     const int32_t* __restrict__ block_tables, int max_blocks,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ ctx, int seq_begin,
     float scale_log2, T* __restrict__ out, int64_t out_stride) {
-  using M = Mfma<T>;
+  using M = Mfma32<T>;
   using v8 = typename M::v8;
-  constexpr int QT = 64 / G;            // query tokens per workgroup
-  constexpr int KT = kChunkKeys;        // keys per tile
-  constexpr int KSTEPS = D / 32;        // k-steps of Q K^T
-  constexpr int NTILE = D / 16;         // 16-wide output column tiles
-  constexpr int KROW = D + 8;           // LDS row stride of K (elements)
-  constexpr int VROW = KT + 8;          // LDS row stride of V^T (elements)
-  constexpr int CPR = D / 8;            // 16-byte chunks per key row
-  constexpr int PER_T = KT * CPR / kChunkThreads;  // chunks per thread per tile
+  using L = ChunkLds<D>;
+  constexpr int QT = kChunkRows / G;   // query tokens per workgroup
+  constexpr int KT = kChunkKeys;
+  constexpr int QSTEPS = D / 16;       // k-steps of K Q^T
+  constexpr int DBLK = D / 32;         // 32-dim blocks of O^T
+  constexpr int CPR = D / 8;           // 16-byte chunks per key row
+  constexpr int PER_T = KT * CPR / kChunkThreads;
   static_assert(PER_T >= 1 && KT * CPR == PER_T * kChunkThreads, "tile split");
-  static_assert(KT % BS == 0 || BS % KT == 0, "tile / block");
-  __shared__ __align__(16) uint16_t Ks[KT * KROW];
-  __shared__ __align__(16) uint16_t Vt[D * VROW];
+  static_assert(KT % BS == 0, "tile / block");
+  extern __shared__ __align__(16) uint16_t chunk_lds[];
+  uint16_t* Ks = chunk_lds;                 // [2][KT][KROW]
+  uint16_t* Vs = chunk_lds + 2 * L::KBUF;   // [2][KT][VROW]
 
   const int seq = seq_begin + (int)blockIdx.z;
   const int kvh = blockIdx.y;
@@ -594,161 +619,196 @@ __global__ __launch_bounds__(kChunkThreads) void attn_chunk_mfma_kernel(
   const int qt0 = (int)blockIdx.x * QT;
   if (qt0 >= qlen) return;
   const int ctxlen = min(ctx[seq], max_blocks * BS);
-  const int pos0 = ctxlen - qlen;                        // position of chunk row 0
-  const int kend = max(0, min(ctxlen, pos0 + qt0 + QT));  // keys [0, kend)
+  const int pos0 = ctxlen - qlen;                                  // position of chunk row 0
+  const int kend = max(0, min(ctxlen, pos0 + min(qt0 + QT, qlen)));  // keys [0, kend)
   if (kend <= 0) return;
+  const int ntiles = (kend + KT - 1) / KT;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int lq = lane & 15;        // query index within the wavefront (S^T / P rows)
-  const int lk = lane >> 4;        // k-group of the lane
+  const int lr = lane & 31;        // this lane's query column / key row
+  const int h = lane >> 5;         // half of the wavefront
   const int64_t tok_stride = (int64_t)num_kv_heads * D;
   const int32_t* __restrict__ bt = block_tables + (int64_t)seq * max_blocks;
 
-  // Q^T operand: query row (16w + lq) -> (token, head in group).
-  const int row = 16 * wave + lq;
+  // This lane's query row (the B-operand column of K Q^T).
+  const int row = 32 * wave + lr;
   const int qtok = qt0 + row % QT;
   const int qg = row / QT;
-  const int qpos = pos0 + qtok;    // causal limit of this lane's query (S^T layout)
-  v8 qf[KSTEPS];
+  const int qpos = pos0 + qtok;
+  v8 qf[QSTEPS];
   {
-    const T* qp = q + (int64_t)(q0 + min(qtok, qlen - 1)) * q_stride + (int64_t)(kvh * G + qg) * D +
-                  8 * lk;
+    const T* qp = q + (int64_t)(q0 + min(qtok, qlen - 1)) * q_stride +
+                  (int64_t)(kvh * G + qg) * D + 8 * h;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = M::from_bits(load16(qp + 32 * ks));
+    for (int st = 0; st < QSTEPS; ++st) qf[st] = __builtin_bit_cast(v8, load16(qp + 16 * st));
   }
 
-  // Loader: thread chunk c = tid + 256 u -> (key c / CPR, dims 8 (c % CPR) ..).
-  auto block_id = [&](int k) {
-    int b = bt[min(k, kend - 1) / BS];
-    return (b < 0 || b >= num_cache_blocks) ? 0 : b;
-  };
-  auto load_tile = [&](int k0, const int* ids, uint4* kr, uint4* vr) {
+  // Loader: thread chunk c = tid + 256 u -> (tile key c / CPR, dims 8 (c % CPR) ..).
+  // Tiles start on block boundaries, so a chunk's row inside its block and
+  // its LDS offsets are fixed; only the block id changes per tile (clamped
+  // to the last needed block: rows past kend are loaded from it and then
+  // zero-filled, never used).
+  int64_t goff[PER_T];
+  int koff[PER_T], voff[PER_T], tkey[PER_T];
+#pragma unroll
+  for (int u = 0; u < PER_T; ++u) {
+    const int c = threadIdx.x + kChunkThreads * u;
+    tkey[u] = c / CPR;
+    goff[u] = (int64_t)(tkey[u] % BS) * tok_stride + (int64_t)kvh * D + 8 * (c % CPR);
+    koff[u] = tkey[u] * L::KROW + 8 * (c % CPR);
+    voff[u] = tkey[u] * L::VROW + 8 * (c % CPR);
+  }
+  const int last_blk = (kend - 1) / BS;
+  auto tile_ids = [&](int k0, int* ids) {
 #pragma unroll
     for (int u = 0; u < PER_T; ++u) {
-      const int c = threadIdx.x + kChunkThreads * u;
-      const int key = min(k0 + c / CPR, kend - 1);
-      const int64_t off = ((int64_t)ids[u] * BS + key % BS) * tok_stride + (int64_t)kvh * D +
-                          8 * (c % CPR);
+      // CPR == 16: chunk u of every thread lies in block u of the tile
+      const int blk = CPR == 16 ? k0 / BS + u : (k0 + tkey[u]) / BS;
+      const int b = bt[min(blk, last_blk)];
+      ids[u] = (b < 0 || b >= num_cache_blocks) ? 0 : b;
+    }
+  };
+  const int64_t blk_elems = (int64_t)BS * tok_stride;
+  auto load_tile = [&](const int* ids, uint4* kr, uint4* vr) {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int64_t off = (int64_t)ids[u] * blk_elems + goff[u];
       kr[u] = load16(kc + off);
       vr[u] = load16(vc + off);
     }
   };
-  auto tile_ids = [&](int k0, int* ids) {
+  auto store_tile = [&](int buf, int k0, const uint4* kr, const uint4* vr) {
+    uint16_t* kd = Ks + buf * L::KBUF;
+    uint16_t* vd = Vs + buf * L::VBUF;
+    if (k0 + KT <= kend) {        // uniform: the whole tile is live
 #pragma unroll
-    for (int u = 0; u < PER_T; ++u)
-      ids[u] = block_id(k0 + (threadIdx.x + kChunkThreads * u) / CPR);
-  };
-
-  f32x4_t o[NTILE];
+      for (int u = 0; u < PER_T; ++u) {
+        store16(kd + koff[u], kr[u]);
+        store16(vd + voff[u], vr[u]);
+      }
+    } else {
 #pragma unroll
-  for (int t = 0; t < NTILE; ++t) o[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run = kNegBig, l_run = 0.0f;
-
-  int ids_cur[PER_T], ids_nxt[PER_T];
-  uint4 kcur[PER_T], vcur[PER_T], knx[PER_T], vnx[PER_T];
-  tile_ids(0, ids_cur);
-  load_tile(0, ids_cur, kcur, vcur);
-  tile_ids(KT, ids_nxt);
-
-  for (int k0 = 0; k0 < kend; k0 += KT) {
-    // Next tile's K/V (clamped, always issued) and the ids of the one after.
-    load_tile(k0 + KT, ids_nxt, knx, vnx);
-    int ids_nn[PER_T];
-    tile_ids(k0 + 2 * KT, ids_nn);
-    __builtin_amdgcn_sched_barrier(0);
-
-    __syncthreads();  // the previous tile's LDS reads are done
-#pragma unroll
-    for (int u = 0; u < PER_T; ++u) {
-      const int c = threadIdx.x + kChunkThreads * u;
-      const int key = c / CPR, d0 = 8 * (c % CPR);
-      const bool live = k0 + key < kend;
-      const uint4 kz = live ? kcur[u] : make_uint4(0, 0, 0, 0);
-      const uint4 vz = live ? vcur[u] : make_uint4(0, 0, 0, 0);
-      store16(&Ks[key * KROW + d0], kz);
-      const uint32_t w[4] = {vz.x, vz.y, vz.z, vz.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        Vt[(d0 + 2 * j) * VROW + key] = (uint16_t)(w[j] & 0xffffu);
-        Vt[(d0 + 2 * j + 1) * VROW + key] = (uint16_t)(w[j] >> 16);
+      for (int u = 0; u < PER_T; ++u) {
+        const bool live = k0 + tkey[u] < kend;
+        store16(kd + koff[u], live ? kr[u] : make_uint4(0, 0, 0, 0));
+        store16(vd + voff[u], live ? vr[u] : make_uint4(0, 0, 0, 0));
       }
     }
-    __syncthreads();
+  };
 
-    // S^T = K Q^T for keys k0 .. k0+15 (s0) and k0+16 .. k0+31 (s1).
-    f32x4_t s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x16_t o[DBLK];
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      const v8 a0 = M::from_bits(*reinterpret_cast<const uint4*>(&Ks[lq * KROW + 32 * ks + 8 * lk]));
-      const v8 a1 =
-          M::from_bits(*reinterpret_cast<const uint4*>(&Ks[(16 + lq) * KROW + 32 * ks + 8 * lk]));
-      s0 = M::run(a0, qf[ks], s0);
-      s1 = M::run(a1, qf[ks], s1);
+  for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
+  float m_run = kNegBig, l_run = 0.0f;
+
+  // First key of the tile where some row of this wavefront needs masking:
+  // its rows are consecutive tokens from wq0 (QT >= 32) or a tile start.
+  const int wq0 = qt0 + (QT >= 32 ? (32 * wave) % QT : 0);
+  const int mask_from = min(kend, pos0 + wq0 + 1);
+
+  int ids[PER_T];
+  uint4 kr[PER_T], vr[PER_T];
+  tile_ids(0, ids);
+  load_tile(ids, kr, vr);
+  store_tile(0, 0, kr, vr);
+  tile_ids(KT, ids);
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int k0 = it * KT;
+    // Next tile into registers (past the end: a clamped reload, never used).
+    load_tile(ids, kr, vr);
+    tile_ids(k0 + 2 * KT, ids);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const uint16_t* kb_lds = Ks + buf * L::KBUF;
+    const uint16_t* vb_lds = Vs + buf * L::VBUF;
+    // S^T for the two 32-key halves of the tile (raw scores).
+    f32x16_t s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const uint16_t* krow = kb_lds + (32 * kb + lr) * L::KROW + 8 * h;
+      s[kb] = M::run(__builtin_bit_cast(v8, *reinterpret_cast<const uint4*>(krow)), qf[0],
+                     f32x16_t{});
+#pragma unroll
+      for (int st = 1; st < QSTEPS; ++st)
+        s[kb] = M::run(__builtin_bit_cast(v8, *reinterpret_cast<const uint4*>(krow + 16 * st)),
+                       qf[st], s[kb]);
     }
-    float sv[8];
+    // Causal / range mask, only on tiles that reach it (uniform branch).
+    if (k0 + KT > mask_from) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int ka = k0 + 4 * lk + r, kb = k0 + 16 + 4 * lk + r;
-      sv[r] = (ka <= qpos && ka < kend) ? s0[r] * scale_log2 : -__builtin_inff();
-      sv[4 + r] = (kb <= qpos && kb < kend) ? s1[r] * scale_log2 : -__builtin_inff();
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = k0 + 32 * kb + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (!(key <= qpos && key < kend)) s[kb][i] = kNegBig;
+        }
     }
-    float mx = sv[0];
+    // Online softmax in log2 units; masked scores give exp2(-huge) = 0.
+    float mx = kNegBig;
 #pragma unroll
-    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
+    const float m_new = fmaxf(m_run, mx * scale_log2);
     const float alpha = fast_exp2(m_run - m_new);
     m_run = m_new;
-    uint32_t pw[4] = {0u, 0u, 0u, 0u};
     float psum = 0.0f;
+    uint32_t pw[2][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float p = fast_exp2(sv[j] - m_new);
-      psum += p;
-      pw[j >> 1] |= (uint32_t)M::to_bits(p) << (16 * (j & 1));
-    }
-    const v8 pa = M::from_bits(make_uint4(pw[0], pw[1], pw[2], pw[3]));
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const float p0 = fast_exp2(fmaf(s[kb][i], scale_log2, -m_new));
+        const float p1 = fast_exp2(fmaf(s[kb][i + 1], scale_log2, -m_new));
+        psum += p0 + p1;
+        pw[kb][i >> 1] = M::pack2(p0, p1);
+      }
     l_run = l_run * alpha + psum;
-    // O rows are queries 4 lk + r: fetch their rescale factors.
+    if (__ballot(alpha != 1.0f)) {   // some row's max moved: rescale O (uniform branch)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float ar = __shfl(alpha, 4 * lk + r);
+      for (int b = 0; b < DBLK; ++b)
 #pragma unroll
-      for (int t = 0; t < NTILE; ++t) o[t][r] *= ar;
+        for (int i = 0; i < 16; ++i) o[b][i] *= alpha;
     }
+    // O^T += V^T P^T, four 16-key steps.
 #pragma unroll
-    for (int t = 0; t < NTILE; ++t) {
-      const uint16_t* vrow = &Vt[(16 * t + lq) * VROW];
-      const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * lk);
-      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * lk);
-      o[t] = M::run(pa, M::from_bits(make_uint4(lo.x, lo.y, hi.x, hi.y)), o[t]);
-    }
-
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t* pp = &pw[t >> 1][4 * (t & 1)];
+      const v8 pb = __builtin_bit_cast(v8, make_uint4(pp[0], pp[1], pp[2], pp[3]));
+      const int kr0 = 16 * t + 4 * h + ((lane & 15) >> 2);
+      const int dsub = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
-    for (int u = 0; u < PER_T; ++u) {
-      kcur[u] = knx[u];
-      vcur[u] = vnx[u];
-      ids_nxt[u] = ids_nn[u];
+      for (int b = 0; b < DBLK; ++b) {
+        const uint16_t* vp = vb_lds + kr0 * L::VROW + 32 * b + dsub;
+        const i16x4_t lo = lds_read_tr16(vp);
+        const i16x4_t hi = lds_read_tr16(vp + 8 * L::VROW);
+        const i16x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[b] = M::run(__builtin_bit_cast(v8, a), pb, o[b]);
+      }
     }
+    store_tile(buf ^ 1, k0 + KT, kr, vr);
+    __syncthreads();
   }
 
-  // Row sums: each query's four lanes hold partial sums of their keys.
-  l_run += __shfl_xor(l_run, 16);
+  // Row sum over both halves of the wavefront, then write this lane's
+  // query row: O^T slot i of block b is dim 32 b + 8 (i / 4) + 4 h + i % 4.
   l_run += __shfl_xor(l_run, 32);
+  if (qtok >= qlen) return;
+  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  T* op = out + (int64_t)(q0 + qtok) * out_stride + (int64_t)(kvh * G + qg) * D + 4 * h;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int qi = 4 * lk + r;
-    const float lr = __shfl(l_run, qi);
-    const float inv = lr > 0.0f ? 1.0f / lr : 0.0f;
-    const int orow = 16 * wave + qi;
-    const int otok = qt0 + orow % QT;
-    if (otok < qlen) {
-      T* op = out + (int64_t)(q0 + otok) * out_stride + (int64_t)(kvh * G + orow / QT) * D + lq;
+  for (int b = 0; b < DBLK; ++b)
 #pragma unroll
-      for (int t = 0; t < NTILE; ++t) elem<T>::store(op + 16 * t, o[t][r] * inv);
-    }
-  }
+    for (int g4 = 0; g4 < 4; ++g4)
+      *reinterpret_cast<uint2*>(op + 32 * b + 8 * g4) =
+          make_uint2(M::pack2(o[b][4 * g4] * inv, o[b][4 * g4 + 1] * inv),
+                     M::pack2(o[b][4 * g4 + 2] * inv, o[b][4 * g4 + 3] * inv));
 }
 
 // Merge the partitions of one (row, query head); rows with a single
@@ -967,9 +1027,16 @@ static int dispatch(lv_dtype dt, int D, int G, int BS, const LaunchArgs& a, cons
 template <typename T, int D, int G>
 static void launch_chunk_kernel(const LaunchArgs& a, const int32_t* cu, int seq_begin, int n_seqs,
                                 int max_query_len) {
-  constexpr int QT = 64 / G;
+  constexpr int QT = kChunkRows / G;
+  constexpr size_t lds = ChunkLds<D>::BYTES;
+  static bool lds_raised = false;   // > 64 KiB of dynamic LDS needs an opt-in per kernel
+  if (!lds_raised) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_mfma_kernel<T, D, G, 16>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    lds_raised = true;
+  }
   const dim3 grid((max_query_len + QT - 1) / QT, a.num_kv_heads, n_seqs);
-  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16>), grid, dim3(kChunkThreads), 0, a.st,
+  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16>), grid, dim3(kChunkThreads), lds, a.st,
                      (const T*)a.q, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.num_kv_heads,
                      a.num_cache_blocks, a.bt, a.max_blocks, cu, a.ctx, seq_begin, a.scale_log2,
                      (T*)a.out, a.out_stride);
