@@ -576,18 +576,27 @@ template <> struct Mfma32<f16> {
 
 constexpr int kChunkThreads = 256;
 constexpr int kChunkRows = 128;   // (query token, head) rows per workgroup
-constexpr int kChunkKeys = 64;    // keys per LDS tile
-constexpr int kChunkVRow = 160;   // V row stride in LDS (elements): 80 dwords = 16 mod 64 banks
+constexpr int kChunkKeys = 64;    // keys per LDS tile (four 16-token blocks)
 
+// LDS tile of K or V: 64 key rows of D elements, unpadded; 16-byte chunk j of
+// row r holds the row's chunk j ^ (r % CPR).  The XOR swizzle lets 16 rows
+// read at one column land in 16 distinct bank quads.
 template <int D> struct ChunkLds {
-  static constexpr int KROW = D + 8;  // 16-byte pad: 16 consecutive rows hit 16 distinct bank quads
-  static constexpr int VROW = kChunkVRow;
-  static constexpr int KBUF = kChunkKeys * KROW, VBUF = kChunkKeys * VROW;
-  static constexpr size_t BYTES = 2 * (size_t)(KBUF + VBUF) * sizeof(uint16_t);
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int TILE = kChunkKeys * D;       // elements per K or V tile
+  __device__ __forceinline__ static int at(int row, int chunk) {
+    return row * D + 8 * (chunk ^ (row & (CPR - 1)));
+  }
 };
 
 __device__ __forceinline__ i16x4_t lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)p);
+}
+
+// 16 bytes per lane from global memory straight into LDS at wave base + 16 lane.
+__device__ __forceinline__ void load_lds16(const void* g, uint16_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
+                                   0, 0);
 }
 
 template <typename T, int D, int G, int BS>
@@ -604,13 +613,14 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
   constexpr int KT = kChunkKeys;
   constexpr int QSTEPS = D / 16;       // k-steps of K Q^T
   constexpr int DBLK = D / 32;         // 32-dim blocks of O^T
-  constexpr int CPR = D / 8;           // 16-byte chunks per key row
-  constexpr int PER_T = KT * CPR / kChunkThreads;
-  static_assert(PER_T >= 1 && KT * CPR == PER_T * kChunkThreads, "tile split");
-  static_assert(KT % BS == 0, "tile / block");
-  extern __shared__ __align__(16) uint16_t chunk_lds[];
-  uint16_t* Ks = chunk_lds;                 // [2][KT][KROW]
-  uint16_t* Vs = chunk_lds + 2 * L::KBUF;   // [2][KT][VROW]
+  constexpr int CPR = L::CPR;
+  constexpr int RPI = 64 / CPR;        // key rows per wave-wide 1 KiB load
+  constexpr int LPW = BS / RPI;        // loads per wavefront per tile (one block each)
+  static_assert(BS == 16 && KT == 4 * BS, "each of the 4 wavefronts stages one block");
+  // One LDS object per stage and operand: a load in flight into one stage
+  // provably does not alias the reads of the other, so the compiler does not
+  // make those reads wait for it.
+  __shared__ __align__(16) uint16_t Ks0[L::TILE], Ks1[L::TILE], Vs0[L::TILE], Vs1[L::TILE];
 
   const int seq = seq_begin + (int)blockIdx.z;
   const int kvh = blockIdx.y;
@@ -619,11 +629,11 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
   const int qt0 = (int)blockIdx.x * QT;
   if (qt0 >= qlen) return;
   const int ctxlen = min(ctx[seq], max_blocks * BS);
-  const int pos0 = ctxlen - qlen;                                  // position of chunk row 0
+  const int pos0 = ctxlen - qlen;                                    // position of chunk row 0
   const int kend = max(0, min(ctxlen, pos0 + min(qt0 + QT, qlen)));  // keys [0, kend)
   if (kend <= 0) return;
   const int ntiles = (kend + KT - 1) / KT;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31;        // this lane's query column / key row
   const int h = lane >> 5;         // half of the wavefront
@@ -643,57 +653,36 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
     for (int st = 0; st < QSTEPS; ++st) qf[st] = __builtin_bit_cast(v8, load16(qp + 16 * st));
   }
 
-  // Loader: thread chunk c = tid + 256 u -> (tile key c / CPR, dims 8 (c % CPR) ..).
-  // Tiles start on block boundaries, so a chunk's row inside its block and
-  // its LDS offsets are fixed; only the block id changes per tile (clamped
-  // to the last needed block: rows past kend are loaded from it and then
-  // zero-filled, never used).
-  int64_t goff[PER_T];
-  int koff[PER_T], voff[PER_T], tkey[PER_T];
+  // Staging: wavefront w loads block w of the tile (rows 16w..16w+15) with
+  // LPW wave-wide loads; lane l of load u fills LDS slot l % CPR of row
+  // 16w + RPI u + l / CPR, i.e. the row's chunk (l % CPR) ^ (row % CPR).
+  int64_t goff[LPW];
 #pragma unroll
-  for (int u = 0; u < PER_T; ++u) {
-    const int c = threadIdx.x + kChunkThreads * u;
-    tkey[u] = c / CPR;
-    goff[u] = (int64_t)(tkey[u] % BS) * tok_stride + (int64_t)kvh * D + 8 * (c % CPR);
-    koff[u] = tkey[u] * L::KROW + 8 * (c % CPR);
-    voff[u] = tkey[u] * L::VROW + 8 * (c % CPR);
+  for (int u = 0; u < LPW; ++u) {
+    const int r = RPI * u + lane / CPR;            // row inside the block
+    const int chunk = (lane % CPR) ^ ((16 * wave + r) & (CPR - 1));
+    goff[u] = (int64_t)r * tok_stride + (int64_t)kvh * D + 8 * chunk;
   }
   const int last_blk = (kend - 1) / BS;
-  auto tile_ids = [&](int k0, int* ids) {
-#pragma unroll
-    for (int u = 0; u < PER_T; ++u) {
-      // CPR == 16: chunk u of every thread lies in block u of the tile
-      const int blk = CPR == 16 ? k0 / BS + u : (k0 + tkey[u]) / BS;
-      const int b = bt[min(blk, last_blk)];
-      ids[u] = (b < 0 || b >= num_cache_blocks) ? 0 : b;
-    }
-  };
   const int64_t blk_elems = (int64_t)BS * tok_stride;
-  auto load_tile = [&](const int* ids, uint4* kr, uint4* vr) {
+  auto stage = [&](uint16_t* Kst, uint16_t* Vst, int k0) {
+    int b = bt[min(k0 / BS + wave, last_blk)];
+    b = (b < 0 || b >= num_cache_blocks) ? 0 : b;
+    const T* kp = kc + (int64_t)b * blk_elems;
+    const T* vp = vc + (int64_t)b * blk_elems;
+    uint16_t* kd = Kst + 16 * wave * D;
+    uint16_t* vd = Vst + 16 * wave * D;
 #pragma unroll
-    for (int u = 0; u < PER_T; ++u) {
-      const int64_t off = (int64_t)ids[u] * blk_elems + goff[u];
-      kr[u] = load16(kc + off);
-      vr[u] = load16(vc + off);
+    for (int u = 0; u < LPW; ++u) {
+      load_lds16(kp + goff[u], kd + RPI * u * D);
+      load_lds16(vp + goff[u], vd + RPI * u * D);
     }
   };
-  auto store_tile = [&](int buf, int k0, const uint4* kr, const uint4* vr) {
-    uint16_t* kd = Ks + buf * L::KBUF;
-    uint16_t* vd = Vs + buf * L::VBUF;
-    if (k0 + KT <= kend) {        // uniform: the whole tile is live
-#pragma unroll
-      for (int u = 0; u < PER_T; ++u) {
-        store16(kd + koff[u], kr[u]);
-        store16(vd + voff[u], vr[u]);
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < PER_T; ++u) {
-        const bool live = k0 + tkey[u] < kend;
-        store16(kd + koff[u], live ? kr[u] : make_uint4(0, 0, 0, 0));
-        store16(vd + voff[u], live ? vr[u] : make_uint4(0, 0, 0, 0));
-      }
-    }
+  // Rows at or past kend hold data of the clamped block: zero their V so a
+  // zero probability never meets a NaN (their scores are masked).
+  auto zero_tail = [&](uint16_t* Vst, int k0) {
+    for (int c = threadIdx.x; c < KT * CPR; c += kChunkThreads)
+      if (k0 + c / CPR >= kend) store16(Vst + (c / CPR) * D + 8 * (c % CPR), make_uint4(0, 0, 0, 0));
   };
 
   f32x16_t o[DBLK];
@@ -708,35 +697,29 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
   const int wq0 = qt0 + (QT >= 32 ? (32 * wave) % QT : 0);
   const int mask_from = min(kend, pos0 + wq0 + 1);
 
-  int ids[PER_T];
-  uint4 kr[PER_T], vr[PER_T];
-  tile_ids(0, ids);
-  load_tile(ids, kr, vr);
-  store_tile(0, 0, kr, vr);
-  tile_ids(KT, ids);
-  __syncthreads();
+  // Per-lane LDS offsets of the MFMA operands.
+  int koff[2][QSTEPS];       // K rows 32 kb + lr, chunk 2 st + h
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int st = 0; st < QSTEPS; ++st) koff[kb][st] = L::at(32 * kb + lr, 2 * st + h);
+  // V^T transpose reads: 16-lane group reads 4 key rows x 16 dims.
+  const int vrow = 4 * h + ((lane & 15) >> 2);
+  const int vdim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    const int k0 = it * KT;
-    // Next tile into registers (past the end: a clamped reload, never used).
-    load_tile(ids, kr, vr);
-    tile_ids(k0 + 2 * KT, ids);
-    __builtin_amdgcn_sched_barrier(0);
-
-    const uint16_t* kb_lds = Ks + buf * L::KBUF;
-    const uint16_t* vb_lds = Vs + buf * L::VBUF;
-    // S^T for the two 32-key halves of the tile (raw scores).
+  auto compute = [&](const uint16_t* kb_lds, const uint16_t* vb_lds, int k0) {
+    // S^T for the two 32-key halves of the tile (raw scores); all K
+    // operands of a half are read before its MFMA chain.
     f32x16_t s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const uint16_t* krow = kb_lds + (32 * kb + lr) * L::KROW + 8 * h;
-      s[kb] = M::run(__builtin_bit_cast(v8, *reinterpret_cast<const uint4*>(krow)), qf[0],
-                     f32x16_t{});
+      uint4 ka[QSTEPS];
 #pragma unroll
-      for (int st = 1; st < QSTEPS; ++st)
-        s[kb] = M::run(__builtin_bit_cast(v8, *reinterpret_cast<const uint4*>(krow + 16 * st)),
-                       qf[st], s[kb]);
+      for (int st = 0; st < QSTEPS; ++st)
+        ka[st] = *reinterpret_cast<const uint4*>(kb_lds + koff[kb][st]);
+      s[kb] = M::run(__builtin_bit_cast(v8, ka[0]), qf[0], f32x16_t{});
+#pragma unroll
+      for (int st = 1; st < QSTEPS; ++st) s[kb] = M::run(__builtin_bit_cast(v8, ka[st]), qf[st], s[kb]);
     }
     // Causal / range mask, only on tiles that reach it (uniform branch).
     if (k0 + KT > mask_from) {
@@ -776,24 +759,53 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[b][i] *= alpha;
     }
-    // O^T += V^T P^T, four 16-key steps.
+    // O^T += V^T P^T, four 16-key steps; the step's transpose reads are
+    // issued together ahead of its MFMAs.
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const uint32_t* pp = &pw[t >> 1][4 * (t & 1)];
       const v8 pb = __builtin_bit_cast(v8, make_uint4(pp[0], pp[1], pp[2], pp[3]));
-      const int kr0 = 16 * t + 4 * h + ((lane & 15) >> 2);
-      const int dsub = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      const int r0 = 16 * t + vrow;
+      i16x4_t lo[DBLK], hi[DBLK];
 #pragma unroll
       for (int b = 0; b < DBLK; ++b) {
-        const uint16_t* vp = vb_lds + kr0 * L::VROW + 32 * b + dsub;
-        const i16x4_t lo = lds_read_tr16(vp);
-        const i16x4_t hi = lds_read_tr16(vp + 8 * L::VROW);
-        const i16x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        const int dim = 32 * b + vdim;
+        lo[b] = lds_read_tr16(vb_lds + L::at(r0, dim >> 3) + (dim & 7));
+        hi[b] = lds_read_tr16(vb_lds + L::at(r0 + 8, dim >> 3) + (dim & 7));
+      }
+#pragma unroll
+      for (int b = 0; b < DBLK; ++b) {
+        const i16x8_t a = __builtin_shufflevector(lo[b], hi[b], 0, 1, 2, 3, 4, 5, 6, 7);
         o[b] = M::run(__builtin_bit_cast(v8, a), pb, o[b]);
       }
     }
-    store_tile(buf ^ 1, k0 + KT, kr, vr);
+  };
+
+  // One step: start loading the next tile into the other stage, compute
+  // this one, then wait for the loads and make them visible to all.
+  auto step = [&](uint16_t* Kc, uint16_t* Vc, uint16_t* Kn, uint16_t* Vn, int it) {
+    const int k0 = it * KT;
+    const bool more = it + 1 < ntiles;
+    if (more) stage(Kn, Vn, k0 + KT);
+    compute(Kc, Vc, k0);
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's LDS loads have landed
+    __syncthreads();                 // ... and everyone's; the current stage is free
+    if (more && k0 + 2 * KT > kend) {
+      zero_tail(Vn, k0 + KT);
+      __syncthreads();
+    }
+  };
+  stage(Ks0, Vs0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (KT > kend) {
+    zero_tail(Vs0, 0);
     __syncthreads();
+  }
+  for (int it = 0; it < ntiles; it += 2) {
+    step(Ks0, Vs0, Ks1, Vs1, it);
+    if (it + 1 >= ntiles) break;
+    step(Ks1, Vs1, Ks0, Vs0, it + 1);
   }
 
   // Row sum over both halves of the wavefront, then write this lane's
@@ -1028,15 +1040,8 @@ template <typename T, int D, int G>
 static void launch_chunk_kernel(const LaunchArgs& a, const int32_t* cu, int seq_begin, int n_seqs,
                                 int max_query_len) {
   constexpr int QT = kChunkRows / G;
-  constexpr size_t lds = ChunkLds<D>::BYTES;
-  static bool lds_raised = false;   // > 64 KiB of dynamic LDS needs an opt-in per kernel
-  if (!lds_raised) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_mfma_kernel<T, D, G, 16>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    lds_raised = true;
-  }
   const dim3 grid((max_query_len + QT - 1) / QT, a.num_kv_heads, n_seqs);
-  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16>), grid, dim3(kChunkThreads), lds, a.st,
+  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16>), grid, dim3(kChunkThreads), 0, a.st,
                      (const T*)a.q, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.num_kv_heads,
                      a.num_cache_blocks, a.bt, a.max_blocks, cu, a.ctx, seq_begin, a.scale_log2,
                      (T*)a.out, a.out_stride);
