@@ -51,7 +51,7 @@ const char* lv_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int lv_abi_version(void);
-#define LV_ABI_VERSION 1
+#define LV_ABI_VERSION 2
 
 /* ------------------------------------------------------------------------
  * (1) Ragged-batch packing.
@@ -196,13 +196,19 @@ int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
  *                         fixed-order fp32 arithmetic defined in sampler.hip
  *                         (bit-reproducible; the CPU restatement matches it
  *                         bit for bit).
- * temperature_dev / uniform_dev: fp32 [B]; uniform may be NULL if every row
- * is greedy.  out_ids_dev: int64 [B].
+ * temperature_dev / uniform_dev: fp32 [B] (uniform is read only for rows with
+ * temperature > 0; pass zeros when every row is greedy).  out_ids_dev:
+ * int64 [B].  workspace: device scratch of at least
+ * lv_sample_workspace_size(num_rows, vocab_size) bytes (no initialisation
+ * needed; calls that overlap on one workspace race: use one per stream).
+ * Two kernels are enqueued on `stream`.
  */
+size_t lv_sample_workspace_size(int64_t num_rows, int64_t vocab_size);
+
 int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
               int64_t row_stride, const float* temperature_dev,
-              const float* uniform_dev, int64_t* out_ids_dev, lv_dtype dtype,
-              void* stream);
+              const float* uniform_dev, int64_t* out_ids_dev, void* workspace_dev,
+              size_t workspace_bytes, lv_dtype dtype, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused layer prologue / epilogue work (the elementwise ops the reference

@@ -1,5 +1,13 @@
-// Fused greedy / temperature sampler over [B, V] logits, one workgroup per
-// row.
+// Fused greedy / temperature sampler over [B, V] logits.
+//
+// Two launches.  sampler_segments_kernel spreads every row over
+// ceil(nseg / SPW) workgroups (SPW = 4 wavefronts x UNROLL segments in
+// flight x GROUPS rounds, one wavefront per segment; default 16):
+// greedy rows leave one (max, index) candidate per workgroup, temperature
+// rows leave (m_s, sigma_s) per segment (defined below).  Each segment's
+// arithmetic is self-contained, so how segments are spread over workgroups
+// does not change any bit.  sampler_search_kernel (one workgroup per row)
+// merges the candidates or runs the cross-segment part and the search.
 //
 // Greedy rows (temperature 0) follow _argmax_kernel / torch.argmax
 // (reference litevllm/layers/sampler.py:60-84, 111-124): the first index of
@@ -35,15 +43,14 @@
 // Every sum, product and comparison is an IEEE fp32 operation in the order
 // written (this file is compiled with -ffp-contract=off); exp2_det uses only
 // fmaf, rint and exact power-of-two scaling.
+#include <stdlib.h>
+
 #include "lv_common.h"
 
 namespace lv {
 
-constexpr int kSampThreads = 1024;
-constexpr int kSampWaves = kSampThreads / 64;
 constexpr int kSeg = 512;
 constexpr int kMaxSegs = 4096;  // vocab up to 2^21
-constexpr int kUnroll = 4;      // segments in flight per wavefront
 
 // log2(e) rounded to fp32.
 constexpr float kLog2e = 0x1.715476p+0f;
@@ -54,8 +61,11 @@ constexpr float kLog2e = 0x1.715476p+0f;
 // applied by an exact power-of-two multiply.  Inputs below -125 (and NaN)
 // give 0, so no result is subnormal.  Relative error < 2^-22 on [-125, 0].
 __device__ __forceinline__ float exp2_det(float t) {
-  if (!(t >= -125.0f)) return 0.0f;
-  if (t > 0.0f) t = 0.0f;
+  // Branch-free form of: t < -125 or NaN -> 0; t > 0 -> t = 0.  For t in
+  // [-125, 0] the clamps leave t unchanged, so every result equals the
+  // plain definition above bit for bit.
+  const bool under = !(t >= -125.0f);
+  t = fmaxf(fminf(t, 0.0f), -125.0f);
   const float n = rintf(t);
   const float f = t - n;  // exact (Sterbenz)
   float p = 0x1.ffcbfcp-17f;
@@ -68,7 +78,7 @@ __device__ __forceinline__ float exp2_det(float t) {
   p = fmaf(p, f, 1.0f);
   const int ni = (int)n;
   const float scale = __uint_as_float((uint32_t)(ni + 127) << 23);
-  return p * scale;
+  return under ? 0.0f : p * scale;
 }
 
 // Load elements [512 s + 8 lane, +8) of a row as fp32; entries past V are
@@ -116,50 +126,73 @@ __device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi)
   return v > bv || (v == bv && i < bi);
 }
 
-template <typename T>
-__global__ __launch_bounds__(kSampThreads) void sampler_kernel(
-    const T* __restrict__ logits, int64_t V, int64_t row_stride,
-    const float* __restrict__ temperature, const float* __restrict__ uniform,
-    int64_t* __restrict__ out, int vec_ok) {
-  __shared__ float s_m[kMaxSegs];
-  __shared__ float s_w[kMaxSegs];
-  __shared__ float s_gv[kSampWaves];
-  __shared__ int64_t s_gi[kSampWaves];
+constexpr int kSegThreads = 256;
+constexpr int kSegWaves = kSegThreads / 64;
 
+
+struct SampWs {
+  float* m;        // [rows, nseg] segment maxima
+  float* w;        // [rows, nseg] segment sums sigma_s
+  float* bv;       // [rows, split] greedy candidates: value
+  int64_t* bi;     //                                  index
+};
+
+template <typename T, int UNROLL, int GROUPS>
+__global__ __launch_bounds__(kSegThreads) void sampler_segments_kernel(
+    const T* __restrict__ logits, int64_t V, int64_t row_stride,
+    const float* __restrict__ temperature, SampWs ws, int nseg, int split, int vec_ok) {
+  constexpr int kUnroll = UNROLL, kGroups = GROUPS;
+  constexpr int kSegsPerWG = kSegWaves * kUnroll * kGroups;
+  __shared__ float s_gv[kSegWaves];
+  __shared__ int64_t s_gi[kSegWaves];
   const int64_t r = blockIdx.x;
+  const int part = blockIdx.y;
   const T* row = logits + r * row_stride;
-  const int nseg = (int)((V + kSeg - 1) / kSeg);
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const bool vec = vec_ok != 0;
-
   const float temp = temperature[r];
   const float c = kLog2e / temp;
   const bool greedy = !(temp > 0.0f) || !(c <= 3.0e38f);
+  const int sbeg = part * kSegsPerWG;
+  const int send = min(nseg, sbeg + kSegsPerWG);
 
+  // Wavefront w folds segments sbeg + w + 4 i in groups of UNROLL; segment
+  // index of group g, slot u: sbeg + w + 4 (UNROLL g + u).
+  auto seg_of = [&](int g, int u) { return sbeg + wave + kSegWaves * (kUnroll * g + u); };
+  auto load_group = [&](int g, float (*x)[8]) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int s = seg_of(g, u);
+      if (s < send) load_chunk(row, V, s, lane, vec, x[u]);
+    }
+  };
+  float xa[kUnroll][8], xb[kUnroll][8];
   if (greedy) {
     float bv = -__builtin_inff();
     int64_t bi = INT64_MAX;
-    for (int s0 = wave; s0 < nseg; s0 += kUnroll * kSampWaves) {
-      float x[kUnroll][8];
+    auto fold = [&](int g, float (*x)[8]) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        const int s = s0 + u * kSampWaves;
-        if (s < nseg) load_chunk(row, V, s, lane, vec, x[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int s = s0 + u * kSampWaves;
-        if (s < nseg) {
+        const int s = seg_of(g, u);
+        if (s < send) {
           const int64_t e0 = (int64_t)s * kSeg + lane * 8;
 #pragma unroll
           for (int j = 0; j < 8; ++j)
             if (x[u][j] > bv) { bv = x[u][j]; bi = e0 + j; }
         }
       }
+    };
+    load_group(0, xa);
+#pragma unroll
+    for (int g = 0; g < kGroups; g += 2) {
+      if (g + 1 < kGroups) load_group(g + 1, xb);
+      fold(g, xa);
+      if (g + 2 < kGroups) load_group(g + 2, xa);
+      if (g + 1 < kGroups) fold(g + 1, xb);
     }
     // Lanes may hold their best from a later segment than an equal value of
-    // another lane, so the merge is lexicographic on (value, index).
+    // another lane, so merges are lexicographic on (value, index).
 #pragma unroll
     for (int ofs = 32; ofs >= 1; ofs >>= 1) {
       const float ov = __shfl_xor(bv, ofs);
@@ -169,34 +202,73 @@ __global__ __launch_bounds__(kSampThreads) void sampler_kernel(
     if (lane == 0) { s_gv[wave] = bv; s_gi[wave] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
-      for (int w = 1; w < kSampWaves; ++w)
+      for (int w = 1; w < kSegWaves; ++w)
         if (better(s_gv[w], s_gi[w], bv, bi)) { bv = s_gv[w]; bi = s_gi[w]; }
-      out[r] = (bi == INT64_MAX) ? 0 : bi;
+      ws.bv[r * split + part] = bv;
+      ws.bi[r * split + part] = bi;
     }
     return;
   }
-
-  // Phase 1: per-segment max and scanned exp weights.
-  for (int s0 = wave; s0 < nseg; s0 += kUnroll * kSampWaves) {
-    float x[kUnroll][8];
+  // Per-segment max and scanned exp weights.
+  auto fold = [&](int g, float (*x)[8]) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int s = s0 + u * kSampWaves;
-      if (s < nseg) load_chunk(row, V, s, lane, vec, x[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int s = s0 + u * kSampWaves;
-      if (s < nseg) {
+      const int s = seg_of(g, u);
+      if (s < send) {
         float e[8];
         float ms = x[u][0];
 #pragma unroll
         for (int j = 1; j < 8; ++j) ms = fmaxf(ms, x[u][j]);
         ms = group_max<64>(ms);
         const float A = wave_scan_hs(chunk_weights(x[u], ms, c, e), lane);
-        if (lane == 63) { s_m[s] = ms; s_w[s] = A; }
+        if (lane == 63) {
+          ws.m[r * nseg + s] = ms;
+          ws.w[r * nseg + s] = A;
+        }
       }
     }
+  };
+  load_group(0, xa);
+#pragma unroll
+  for (int g = 0; g < kGroups; g += 2) {
+    if (g + 1 < kGroups) load_group(g + 1, xb);
+    fold(g, xa);
+    if (g + 2 < kGroups) load_group(g + 2, xa);
+    if (g + 1 < kGroups) fold(g + 1, xb);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSegThreads) void sampler_search_kernel(
+    const T* __restrict__ logits, int64_t V, int64_t row_stride,
+    const float* __restrict__ temperature, const float* __restrict__ uniform, SampWs ws,
+    int nseg, int split, int64_t* __restrict__ out, int vec_ok) {
+  __shared__ float s_m[kMaxSegs];
+  __shared__ float s_w[kMaxSegs];
+  const int64_t r = blockIdx.x;
+  const T* row = logits + r * row_stride;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const bool vec = vec_ok != 0;
+  const float temp = temperature[r];
+  const float c = kLog2e / temp;
+  const bool greedy = !(temp > 0.0f) || !(c <= 3.0e38f);
+  if (greedy) {
+    if (threadIdx.x == 0) {
+      float bv = -__builtin_inff();
+      int64_t bi = INT64_MAX;
+      for (int p = 0; p < split; ++p)
+        if (better(ws.bv[r * split + p], ws.bi[r * split + p], bv, bi)) {
+          bv = ws.bv[r * split + p];
+          bi = ws.bi[r * split + p];
+        }
+      out[r] = (bi == INT64_MAX) ? 0 : bi;
+    }
+    return;
+  }
+  for (int i = threadIdx.x; i < nseg; i += kSegThreads) {
+    s_m[i] = ws.m[r * nseg + i];
+    s_w[i] = ws.w[r * nseg + i];
   }
   __syncthreads();
   if (wave != 0) return;
@@ -301,9 +373,35 @@ __global__ __launch_bounds__(kSampThreads) void sampler_kernel(
 
 }  // namespace lv
 
+namespace lv {
+// Segments per workgroup of the first kernel (LV_SAMPLER_SPW = 4, 8, 16,
+// 32: a tuning knob; 16 measured best on config 4).
+static inline int samp_spw() {
+  static const int v = [] {
+    const char* e = getenv("LV_SAMPLER_SPW");
+    const int x = e ? atoi(e) : 16;
+    return (x == 4 || x == 8 || x == 16 || x == 32) ? x : 16;
+  }();
+  return v;
+}
+static inline int64_t samp_split(int nseg) { return (nseg + samp_spw() - 1) / samp_spw(); }
+static inline size_t samp_ws_bytes(int64_t rows, int64_t V) {
+  const int64_t nseg = (V + kSeg - 1) / kSeg;
+  const int64_t split = samp_split((int)nseg);
+  return (size_t)rows * (size_t)(split * 16 + nseg * 8) + 256;
+}
+}  // namespace lv
+
+extern "C" size_t lv_sample_workspace_size(int64_t num_rows, int64_t vocab_size) {
+  using namespace lv;
+  if (num_rows <= 0 || vocab_size <= 0 || vocab_size > (int64_t)kSeg * kMaxSegs) return 0;
+  return samp_ws_bytes(num_rows, vocab_size);
+}
+
 extern "C" int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
                          int64_t row_stride, const float* temperature_dev, const float* uniform_dev,
-                         int64_t* out_ids_dev, lv_dtype dtype, void* stream) {
+                         int64_t* out_ids_dev, void* workspace_dev, size_t workspace_bytes,
+                         lv_dtype dtype, void* stream) {
   using namespace lv;
   clear_error();
   LV_REQUIRE(dtype == LV_F32 || dtype == LV_F16 || dtype == LV_BF16, "lv_sample: bad dtype");
@@ -314,22 +412,43 @@ extern "C" int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab
   LV_REQUIRE(row_stride >= vocab_size, "lv_sample: row_stride < vocab_size");
   LV_REQUIRE(logits_dev && temperature_dev && out_ids_dev, "lv_sample: null pointer");
   LV_REQUIRE(uniform_dev, "lv_sample: uniform draws required (pass zeros for all-greedy rows)");
-  const int vec = aligned16(logits_dev) && ((row_stride * (int64_t)dtype_size(dtype)) % 16 == 0);
-  hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)num_rows), block(kSampThreads);
-  switch (dtype) {
-    case LV_BF16:
-      hipLaunchKernelGGL(sampler_kernel<bf16>, grid, block, 0, st, (const bf16*)logits_dev,
-                         vocab_size, row_stride, temperature_dev, uniform_dev, out_ids_dev, vec);
-      break;
-    case LV_F16:
-      hipLaunchKernelGGL(sampler_kernel<f16>, grid, block, 0, st, (const f16*)logits_dev,
-                         vocab_size, row_stride, temperature_dev, uniform_dev, out_ids_dev, vec);
-      break;
-    default:
-      hipLaunchKernelGGL(sampler_kernel<float>, grid, block, 0, st, (const float*)logits_dev,
-                         vocab_size, row_stride, temperature_dev, uniform_dev, out_ids_dev, vec);
-      break;
+  const size_t need = samp_ws_bytes(num_rows, vocab_size);
+  if (!workspace_dev || workspace_bytes < need) {
+    set_error("lv_sample: workspace of %zu bytes required, got %zu", need, workspace_bytes);
+    return LV_ERR_WORKSPACE;
   }
-  return check_launch("lv_sample");
+  const int vec = aligned16(logits_dev) && ((row_stride * (int64_t)dtype_size(dtype)) % 16 == 0);
+  const int nseg = (int)((vocab_size + kSeg - 1) / kSeg);
+  const int split = (int)samp_split(nseg);
+  char* base = (char*)(((uintptr_t)workspace_dev + 255) & ~(uintptr_t)255);
+  SampWs ws;
+  ws.bi = (int64_t*)base;
+  ws.bv = (float*)(base + (size_t)num_rows * split * 8);
+  ws.m = (float*)(base + (size_t)num_rows * split * 12);
+  ws.w = ws.m + (size_t)num_rows * nseg;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid_a((unsigned)num_rows, (unsigned)split), grid_b((unsigned)num_rows);
+  const dim3 block(kSegThreads);
+#define LV_SEG(TT, U, G)                                                                        \
+  hipLaunchKernelGGL((sampler_segments_kernel<TT, U, G>), grid_a, block, 0, st,                 \
+                     (const TT*)logits_dev, vocab_size, row_stride, temperature_dev, ws, nseg,   \
+                     split, vec)
+#define LV_SAMPLE_LAUNCH(TT)                                                                    \
+  switch (samp_spw()) {                                                                         \
+    case 4: LV_SEG(TT, 1, 1); break;                                                            \
+    case 8: LV_SEG(TT, 2, 1); break;                                                            \
+    case 32: LV_SEG(TT, 4, 2); break;                                                           \
+    default: LV_SEG(TT, 4, 1); break;                                                           \
+  }                                                                                             \
+  hipLaunchKernelGGL(sampler_search_kernel<TT>, grid_b, block, 0, st, (const TT*)logits_dev,    \
+                     vocab_size, row_stride, temperature_dev, uniform_dev, ws, nseg, split,      \
+                     out_ids_dev, vec)
+  switch (dtype) {
+    case LV_BF16: LV_SAMPLE_LAUNCH(bf16); break;
+    case LV_F16: LV_SAMPLE_LAUNCH(f16); break;
+    default: LV_SAMPLE_LAUNCH(float); break;
+  }
+#undef LV_SAMPLE_LAUNCH
+#undef LV_SEG
+  return check_launch("sampler kernels");
 }

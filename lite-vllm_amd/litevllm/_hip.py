@@ -17,7 +17,7 @@ LIB_NAME = "liblitevllm_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 LV_F32, LV_F16, LV_BF16 = 0, 1, 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # Every symbol the header declares, with (restype, argtypes).
 _c_i32, _c_i64, _c_f32, _c_p, _c_sz = (
@@ -59,9 +59,11 @@ SIGNATURES: dict[str, tuple] = {
         _c_p, _c_sz,                  # workspace, workspace_bytes
         ctypes.c_int, _c_p,           # dtype, stream
     ]),
+    "lv_sample_workspace_size": (ctypes.c_size_t, [_c_i64, _c_i64]),
     "lv_sample": (ctypes.c_int, [
         _c_p, _c_i64, _c_i64, _c_i64,  # logits, num_rows, vocab_size, row_stride
         _c_p, _c_p, _c_p,              # temperature, uniform, out_ids
+        _c_p, ctypes.c_size_t,         # workspace, workspace_bytes
         ctypes.c_int, _c_p,            # dtype, stream
     ]),
     "lv_add_rms_norm": (ctypes.c_int, [

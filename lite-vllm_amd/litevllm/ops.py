@@ -268,12 +268,15 @@ def pack_inputs(descs: torch.Tensor, block_ids: torch.Tensor, token_ids: torch.T
 
 def sample(logits: torch.Tensor, temperature: torch.Tensor,
            uniform: Optional[torch.Tensor] = None,
-           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+           out: Optional[torch.Tensor] = None,
+           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Greedy (temperature 0) or inverse-CDF temperature sampling per row.
 
     Reference: litevllm/layers/sampler.py:60-187.  logits [B, V] (unit
     stride along V); temperature / uniform: float32 [B] (uniform in [0, 1),
-    may be None when every row is greedy).  Returns int64 [B].
+    may be None when every row is greedy).  Returns int64 [B].  ``workspace``
+    (uint8, >= lv_sample_workspace_size bytes) replaces the per-stream
+    scratch buffer when given.
     """
     dev = logits.device
     for n, t in (("logits", logits), ("temperature", temperature), ("uniform", uniform),
@@ -297,8 +300,18 @@ def sample(logits: torch.Tensor, temperature: torch.Tensor,
     if B == 0:
         return out
     lib = _hip.load()
+    ws_bytes = int(lib.lv_sample_workspace_size(B, V))
+    if workspace is not None:
+        _require_device("workspace", workspace, dev)
+        if workspace.dtype != torch.uint8 or not workspace.is_contiguous() or \
+                workspace.numel() < ws_bytes:
+            raise RuntimeError(f"workspace must be a contiguous uint8 tensor of >= {ws_bytes} bytes")
+        ws = workspace
+    else:
+        ws = _workspace(dev, ws_bytes)
     rc = lib.lv_sample(_ptr(logits), B, V, logits.stride(0), _ptr(temperature), _ptr(uniform),
-                       _ptr(out), _dtype_code(logits), _stream(dev))
+                       _ptr(out), _ptr(ws), 0 if ws is None else ws.numel(),
+                       _dtype_code(logits), _stream(dev))
     _hip.check(rc, "lv_sample")
     return out
 

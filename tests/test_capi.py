@@ -23,7 +23,8 @@ def _declared_functions() -> set[str]:
 def test_header_declares_the_four_pieces():
     names = _declared_functions()
     for fn in ("lv_pack_inputs", "lv_kv_scatter", "lv_paged_attention",
-               "lv_paged_attention_workspace_size", "lv_sample", "lv_last_error",
+               "lv_paged_attention_workspace_size", "lv_sample", "lv_sample_workspace_size",
+               "lv_last_error",
                "lv_abi_version"):
         assert fn in names
 
@@ -44,7 +45,7 @@ def test_host_side_argument_rejection():
     rc = lib.lv_kv_scatter(None, 8, None, 8, None, None, None, 4, 2, 4, 16, 10, _hip.LV_BF16, None)
     assert rc == -1
     assert b"null pointer" in lib.lv_last_error()
-    rc = lib.lv_sample(None, 4, 0, 0, None, None, None, _hip.LV_BF16, None)
+    rc = lib.lv_sample(None, 4, 0, 0, None, None, None, None, 0, _hip.LV_BF16, None)
     assert rc == -1 and b"vocab_size" in lib.lv_last_error()
     rc = lib.lv_paged_attention(None, 0, None, None, 1, None, 1, None, None, 2, 3, 2, 1,
                                 16, 8, 128, 16, 0.1, None, 0, None, 0, _hip.LV_BF16, None)
@@ -78,3 +79,16 @@ def test_ops_refuse_cpu_tensors():
         ops.kv_scatter(k, k, kc, kc.clone(), torch.zeros(2, dtype=torch.int64))
     with pytest.raises(RuntimeError, match="no CPU implementation"):
         ops.sample(torch.zeros(2, 10), torch.zeros(2))
+
+
+def test_sampler_workspace_size_and_rejection():
+    from litevllm import _hip
+    lib = _hip.load()
+    n = lib.lv_sample_workspace_size(256, 151936)
+    assert n >= 256 * (297 * 8 + 5 * 16)
+    assert lib.lv_sample_workspace_size(0, 100) == 0
+    assert lib.lv_sample_workspace_size(4, 0) == 0
+    # too small a workspace is refused before any launch (pointers are dummies
+    # that are never dereferenced on the host)
+    rc = lib.lv_sample(1, 4, 1000, 1000, 1, 1, 1, 1, 8, _hip.LV_BF16, None)
+    assert rc == -3 and b"workspace" in lib.lv_last_error()
