@@ -22,6 +22,8 @@
 
 #include <atomic>
 
+#include <type_traits>
+
 #include "lv_common.h"
 
 namespace lv {
@@ -574,16 +576,16 @@ template <> struct Mfma32<f16> {
   }
 };
 
-constexpr int kChunkThreads = 256;
-constexpr int kChunkRows = 128;   // (query token, head) rows per workgroup
-constexpr int kChunkKeys = 64;    // keys per LDS tile (four 16-token blocks)
+// W wavefronts per workgroup: 32 W (query token, head) rows, and LDS tiles
+// of 16 W keys (one 16-token block staged per wavefront), computed in
+// sub-tiles of 64 keys.
 
-// LDS tile of K or V: 64 key rows of D elements, unpadded; 16-byte chunk j of
-// row r holds the row's chunk j ^ (r % CPR).  The XOR swizzle lets 16 rows
+// LDS tile of K or V: 16 W key rows of D elements, unpadded; 16-byte chunk j
+// of row r holds the row's chunk j ^ (r % CPR).  The XOR swizzle lets 16 rows
 // read at one column land in 16 distinct bank quads.
-template <int D> struct ChunkLds {
+template <int D, int W> struct ChunkLds {
   static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  static constexpr int TILE = kChunkKeys * D;       // elements per K or V tile
+  static constexpr int TILE = 16 * W * D;           // elements per K or V tile
   __device__ __forceinline__ static int at(int row, int chunk) {
     return row * D + 8 * (chunk ^ (row & (CPR - 1)));
   }
@@ -599,8 +601,8 @@ __device__ __forceinline__ void load_lds16(const void* g, uint16_t* lds_wave_bas
                                    0, 0);
 }
 
-template <typename T, int D, int G, int BS>
-__global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
+template <typename T, int D, int G, int BS, int W>
+__global__ __launch_bounds__(64 * W, 8 / W) void attn_chunk_mfma_kernel(
     const T* __restrict__ q, int64_t q_stride,
     const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
     const int32_t* __restrict__ block_tables, int max_blocks,
@@ -608,15 +610,17 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
     float scale_log2, T* __restrict__ out, int64_t out_stride) {
   using M = Mfma32<T>;
   using v8 = typename M::v8;
-  using L = ChunkLds<D>;
-  constexpr int QT = kChunkRows / G;   // query tokens per workgroup
-  constexpr int KT = kChunkKeys;
+  using L = ChunkLds<D, W>;
+  constexpr int kThreads = 64 * W;
+  constexpr int QT = 32 * W / G;       // query tokens per workgroup
+  constexpr int KT = 16 * W;           // keys per LDS tile
+  constexpr int NSUB = KT / 64;        // 64-key sub-tiles per LDS tile
   constexpr int QSTEPS = D / 16;       // k-steps of K Q^T
   constexpr int DBLK = D / 32;         // 32-dim blocks of O^T
   constexpr int CPR = L::CPR;
   constexpr int RPI = 64 / CPR;        // key rows per wave-wide 1 KiB load
   constexpr int LPW = BS / RPI;        // loads per wavefront per tile (one block each)
-  static_assert(BS == 16 && KT == 4 * BS, "each of the 4 wavefronts stages one block");
+  static_assert(BS == 16 && (W == 4 || W == 8), "each wavefront stages one 16-token block");
   // One LDS object per stage and operand: a load in flight into one stage
   // provably does not alias the reads of the other, so the compiler does not
   // make those reads wait for it.
@@ -681,7 +685,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
   // Rows at or past kend hold data of the clamped block: zero their V so a
   // zero probability never meets a NaN (their scores are masked).
   auto zero_tail = [&](uint16_t* Vst, int k0) {
-    for (int c = threadIdx.x; c < KT * CPR; c += kChunkThreads)
+    for (int c = threadIdx.x; c < KT * CPR; c += kThreads)
       if (k0 + c / CPR >= kend) store16(Vst + (c / CPR) * D + 8 * (c % CPR), make_uint4(0, 0, 0, 0));
   };
 
@@ -692,44 +696,59 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
     for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
   float m_run = kNegBig, l_run = 0.0f;
 
-  // First key of the tile where some row of this wavefront needs masking:
-  // its rows are consecutive tokens from wq0 (QT >= 32) or a tile start.
-  const int wq0 = qt0 + (QT >= 32 ? (32 * wave) % QT : 0);
-  const int mask_from = min(kend, pos0 + wq0 + 1);
 
-  // Per-lane LDS offsets of the MFMA operands.
-  int koff[2][QSTEPS];       // K rows 32 kb + lr, chunk 2 st + h
+  // Per-lane LDS offsets of the MFMA operands.  Rows 32 kb + lr share
+  // lr's swizzle (row & (CPR - 1) == lr & (CPR - 1)), so the K offset of
+  // step st is kx[st] plus the constant 32 kb D; the V rows 16 t + vrow
+  // (+ 8) likewise share a swizzle across t.
+  int kx[QSTEPS];
+  {
+    const int y = h ^ (lr & (CPR - 1));   // (2 st + h) ^ sw == 2 st ^ y
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int st = 0; st < QSTEPS; ++st) koff[kb][st] = L::at(32 * kb + lr, 2 * st + h);
-  // V^T transpose reads: 16-lane group reads 4 key rows x 16 dims.
+    for (int st = 0; st < QSTEPS; ++st) kx[st] = lr * D + 8 * ((2 * st) ^ y);
+  }
   const int vrow = 4 * h + ((lane & 15) >> 2);
-  const int vdim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int voff[DBLK][2];
+#pragma unroll
+  for (int b = 0; b < DBLK; ++b) {
+    const int dim = 32 * b + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    voff[b][0] = L::at(vrow, dim >> 3) + (dim & 7);
+    voff[b][1] = L::at(vrow + 8, dim >> 3) + (dim & 7);
+  }
 
-  auto compute = [&](const uint16_t* kb_lds, const uint16_t* vb_lds, int k0) {
-    // S^T for the two 32-key halves of the tile (raw scores); all K
-    // operands of a half are read before its MFMA chain.
+  // Last key each row may see: its causal limit, capped by the key range.
+  const int lim = min(qpos, kend - 1);
+  // MaskT (std::true_type / std::false_type): whether the tile may need the
+  // causal / range mask.  Masked tiles (at most the last two of a
+  // workgroup) run in a loop of their own, so the mask never becomes
+  // straight-line code on the others.
+  auto compute = [&](auto MaskT, const uint16_t* kb_lds, const uint16_t* vb_lds, int k0) {
+    // S^T for the two 32-key halves of the tile (raw scores); K operands
+    // are read four steps at a time ahead of their MFMAs.
     f32x16_t s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      uint4 ka[QSTEPS];
+      const uint16_t* kbase = kb_lds + 32 * kb * D;
+      uint4 ka[4];
 #pragma unroll
-      for (int st = 0; st < QSTEPS; ++st)
-        ka[st] = *reinterpret_cast<const uint4*>(kb_lds + koff[kb][st]);
+      for (int st = 0; st < 4; ++st) ka[st] = *reinterpret_cast<const uint4*>(kbase + kx[st]);
       s[kb] = M::run(__builtin_bit_cast(v8, ka[0]), qf[0], f32x16_t{});
 #pragma unroll
-      for (int st = 1; st < QSTEPS; ++st) s[kb] = M::run(__builtin_bit_cast(v8, ka[st]), qf[st], s[kb]);
+      for (int st = 1; st < QSTEPS; ++st) {
+        if (st + 3 < QSTEPS)
+          ka[(st + 3) & 3] = *reinterpret_cast<const uint4*>(kbase + kx[st + 3]);
+        s[kb] = M::run(__builtin_bit_cast(v8, ka[st & 3]), qf[st], s[kb]);
+      }
     }
-    // Causal / range mask, only on tiles that reach it (uniform branch).
-    if (k0 + KT > mask_from) {
+    // Causal / range mask: slot i of half kb holds key
+    // k0 + 32 kb + 8 (i / 4) + 4 h + i % 4.
+    if constexpr (decltype(MaskT)::value) {
+      const int d = lim - k0 - 4 * h;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = k0 + 32 * kb + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (!(key <= qpos && key < kend)) s[kb][i] = kNegBig;
-        }
+        for (int i = 0; i < 16; ++i)
+          if (32 * kb + 8 * (i >> 2) + (i & 3) > d) s[kb][i] = kNegBig;
     }
     // Online softmax in log2 units; masked scores give exp2(-huge) = 0.
     float mx = kNegBig;
@@ -765,13 +784,11 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
     for (int t = 0; t < 4; ++t) {
       const uint32_t* pp = &pw[t >> 1][4 * (t & 1)];
       const v8 pb = __builtin_bit_cast(v8, make_uint4(pp[0], pp[1], pp[2], pp[3]));
-      const int r0 = 16 * t + vrow;
       i16x4_t lo[DBLK], hi[DBLK];
 #pragma unroll
       for (int b = 0; b < DBLK; ++b) {
-        const int dim = 32 * b + vdim;
-        lo[b] = lds_read_tr16(vb_lds + L::at(r0, dim >> 3) + (dim & 7));
-        hi[b] = lds_read_tr16(vb_lds + L::at(r0 + 8, dim >> 3) + (dim & 7));
+        lo[b] = lds_read_tr16(vb_lds + 16 * t * D + voff[b][0]);
+        hi[b] = lds_read_tr16(vb_lds + 16 * t * D + voff[b][1]);
       }
 #pragma unroll
       for (int b = 0; b < DBLK; ++b) {
@@ -783,11 +800,13 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
 
   // One step: start loading the next tile into the other stage, compute
   // this one, then wait for the loads and make them visible to all.
-  auto step = [&](uint16_t* Kc, uint16_t* Vc, uint16_t* Kn, uint16_t* Vn, int it) {
+  auto step = [&](auto MaskT, uint16_t* Kc, uint16_t* Vc, uint16_t* Kn, uint16_t* Vn, int it) {
     const int k0 = it * KT;
     const bool more = it + 1 < ntiles;
     if (more) stage(Kn, Vn, k0 + KT);
-    compute(Kc, Vc, k0);
+#pragma unroll 1
+    for (int sub = 0; sub < NSUB; ++sub)
+      compute(MaskT, Kc + 64 * sub * D, Vc + 64 * sub * D, k0 + 64 * sub);
     __builtin_amdgcn_s_waitcnt(0);   // this thread's LDS loads have landed
     __syncthreads();                 // ... and everyone's; the current stage is free
     if (more && k0 + 2 * KT > kend) {
@@ -802,10 +821,25 @@ __global__ __launch_bounds__(kChunkThreads, 2) void attn_chunk_mfma_kernel(
     zero_tail(Vs0, 0);
     __syncthreads();
   }
-  for (int it = 0; it < ntiles; it += 2) {
-    step(Ks0, Vs0, Ks1, Vs1, it);
-    if (it + 1 >= ntiles) break;
-    step(Ks1, Vs1, Ks0, Vs0, it + 1);
+  // Tiles [0, nfull) need no mask for any row of the workgroup (its
+  // earliest row sits at position pos0 + qt0); the rest may.
+  const int nfull = min(ntiles, min(kend, pos0 + qt0 + 1) / KT);
+  const std::false_type plain{};
+  const std::true_type masked{};
+  int it = 0;
+  for (; it + 1 < nfull; it += 2) {
+    step(plain, Ks0, Vs0, Ks1, Vs1, it);
+    step(plain, Ks1, Vs1, Ks0, Vs0, it + 1);
+  }
+  if (it < nfull) {
+    step(plain, Ks0, Vs0, Ks1, Vs1, it);
+    ++it;
+  }
+  for (; it < ntiles; ++it) {
+    if (it & 1)
+      step(masked, Ks1, Vs1, Ks0, Vs0, it);
+    else
+      step(masked, Ks0, Vs0, Ks1, Vs1, it);
   }
 
   // Row sum over both halves of the wavefront, then write this lane's
@@ -1036,15 +1070,30 @@ static int dispatch(lv_dtype dt, int D, int G, int BS, const LaunchArgs& a, cons
   }
 }
 
-template <typename T, int D, int G>
-static void launch_chunk_kernel(const LaunchArgs& a, const int32_t* cu, int seq_begin, int n_seqs,
-                                int max_query_len) {
-  constexpr int QT = kChunkRows / G;
+template <typename T, int D, int G, int W>
+static void launch_chunk_kernel_w(const LaunchArgs& a, const int32_t* cu, int seq_begin,
+                                  int n_seqs, int max_query_len) {
+  constexpr int QT = 32 * W / G;
   const dim3 grid((max_query_len + QT - 1) / QT, a.num_kv_heads, n_seqs);
-  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16>), grid, dim3(kChunkThreads), 0, a.st,
+  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16, W>), grid, dim3(64 * W), 0, a.st,
                      (const T*)a.q, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.num_kv_heads,
                      a.num_cache_blocks, a.bt, a.max_blocks, cu, a.ctx, seq_begin, a.scale_log2,
                      (T*)a.out, a.out_stride);
+}
+
+// Wavefronts per chunk workgroup (LV_ATTN_CHUNK_WAVES = 4 or 8).
+static int chunk_waves() {
+  static const int w = env_int("LV_ATTN_CHUNK_WAVES", 4) == 8 ? 8 : 4;
+  return w;
+}
+
+template <typename T, int D, int G>
+static void launch_chunk_kernel(const LaunchArgs& a, const int32_t* cu, int seq_begin, int n_seqs,
+                                int max_query_len) {
+  if (chunk_waves() == 8)
+    launch_chunk_kernel_w<T, D, G, 8>(a, cu, seq_begin, n_seqs, max_query_len);
+  else
+    launch_chunk_kernel_w<T, D, G, 4>(a, cu, seq_begin, n_seqs, max_query_len);
 }
 
 template <typename T, int D>
