@@ -576,6 +576,8 @@ template <> struct Mfma32<f16> {
   }
 };
 
+constexpr int kXcds = 8;   // XCDs of an MI355X (workgroups are dispatched round-robin over them)
+
 // W wavefronts per workgroup: 32 W (query token, head) rows, and LDS tiles
 // of 16 W keys (one 16-token block staged per wavefront), computed in
 // sub-tiles of 64 keys.
@@ -601,20 +603,21 @@ __device__ __forceinline__ void load_lds16(const void* g, uint16_t* lds_wave_bas
                                    0, 0);
 }
 
-template <typename T, int D, int G, int BS, int W>
-__global__ __launch_bounds__(64 * W, 8 / W) void attn_chunk_mfma_kernel(
+template <typename T, int D, int G, int BS, int W, int BPW>
+__global__ __launch_bounds__(64 * W, 8 / (W * BPW)) void attn_chunk_mfma_kernel(
     const T* __restrict__ q, int64_t q_stride,
     const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
     const int32_t* __restrict__ block_tables, int max_blocks,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ ctx, int seq_begin,
-    float scale_log2, T* __restrict__ out, int64_t out_stride) {
+    int nq_tiles, int num_groups, float scale_log2, T* __restrict__ out, int64_t out_stride) {
   using M = Mfma32<T>;
   using v8 = typename M::v8;
-  using L = ChunkLds<D, W>;
+  using L = ChunkLds<D, W * BPW>;
   constexpr int kThreads = 64 * W;
   constexpr int QT = 32 * W / G;       // query tokens per workgroup
-  constexpr int KT = 16 * W;           // keys per LDS tile
+  constexpr int KT = 16 * W * BPW;     // keys per LDS tile
   constexpr int NSUB = KT / 64;        // 64-key sub-tiles per LDS tile
+  static_assert(NSUB == 1 || NSUB == 2, "one or two 64-key sub-tiles");
   constexpr int QSTEPS = D / 16;       // k-steps of K Q^T
   constexpr int DBLK = D / 32;         // 32-dim blocks of O^T
   constexpr int CPR = L::CPR;
@@ -626,11 +629,20 @@ __global__ __launch_bounds__(64 * W, 8 / W) void attn_chunk_mfma_kernel(
   // make those reads wait for it.
   __shared__ __align__(16) uint16_t Ks0[L::TILE], Ks1[L::TILE], Vs0[L::TILE], Vs1[L::TILE];
 
-  const int seq = seq_begin + (int)blockIdx.z;
-  const int kvh = blockIdx.y;
+  // XCD-aware order: workgroups are dispatched round-robin over the XCDs
+  // (id % kXcds), so workgroup id w serves (sequence, kv head) group
+  // (w / kXcds / nq) * kXcds + w % kXcds and query tile (w / kXcds) % nq:
+  // all query tiles of one group run on one XCD and share its L2 copy of
+  // the group's K/V, and consecutive groups alternate XCDs.
+  const int wg = (int)blockIdx.x;
+  const int slot = wg / kXcds;
+  const int grp = (slot / nq_tiles) * kXcds + wg % kXcds;
+  if (grp >= num_groups) return;
+  const int kvh = grp % num_kv_heads;
+  const int seq = seq_begin + grp / num_kv_heads;
   const int q0 = cu[seq];
   const int qlen = cu[seq + 1] - q0;
-  const int qt0 = (int)blockIdx.x * QT;
+  const int qt0 = (slot % nq_tiles) * QT;
   if (qt0 >= qlen) return;
   const int ctxlen = min(ctx[seq], max_blocks * BS);
   const int pos0 = ctxlen - qlen;                                    // position of chunk row 0
@@ -664,22 +676,27 @@ __global__ __launch_bounds__(64 * W, 8 / W) void attn_chunk_mfma_kernel(
 #pragma unroll
   for (int u = 0; u < LPW; ++u) {
     const int r = RPI * u + lane / CPR;            // row inside the block
-    const int chunk = (lane % CPR) ^ ((16 * wave + r) & (CPR - 1));
+    const int chunk = (lane % CPR) ^ (r & (CPR - 1));  // 16-row blocks keep row & 15
     goff[u] = (int64_t)r * tok_stride + (int64_t)kvh * D + 8 * chunk;
   }
   const int last_blk = (kend - 1) / BS;
   const int64_t blk_elems = (int64_t)BS * tok_stride;
+  // Wavefront w stages blocks w, w + W, ... (BPW of them) of the tile.
   auto stage = [&](uint16_t* Kst, uint16_t* Vst, int k0) {
-    int b = bt[min(k0 / BS + wave, last_blk)];
-    b = (b < 0 || b >= num_cache_blocks) ? 0 : b;
-    const T* kp = kc + (int64_t)b * blk_elems;
-    const T* vp = vc + (int64_t)b * blk_elems;
-    uint16_t* kd = Kst + 16 * wave * D;
-    uint16_t* vd = Vst + 16 * wave * D;
 #pragma unroll
-    for (int u = 0; u < LPW; ++u) {
-      load_lds16(kp + goff[u], kd + RPI * u * D);
-      load_lds16(vp + goff[u], vd + RPI * u * D);
+    for (int j = 0; j < BPW; ++j) {
+      const int blk = wave + W * j;
+      int b = bt[min(k0 / BS + blk, last_blk)];
+      b = (b < 0 || b >= num_cache_blocks) ? 0 : b;
+      const T* kp = kc + (int64_t)b * blk_elems;
+      const T* vp = vc + (int64_t)b * blk_elems;
+      uint16_t* kd = Kst + 16 * blk * D;
+      uint16_t* vd = Vst + 16 * blk * D;
+#pragma unroll
+      for (int u = 0; u < LPW; ++u) {
+        load_lds16(kp + goff[u], kd + RPI * u * D);
+        load_lds16(vp + goff[u], vd + RPI * u * D);
+      }
     }
   };
   // Rows at or past kend hold data of the clamped block: zero their V so a
@@ -716,70 +733,78 @@ __global__ __launch_bounds__(64 * W, 8 / W) void attn_chunk_mfma_kernel(
     voff[b][1] = L::at(vrow + 8, dim >> 3) + (dim & 7);
   }
 
-  // Last key each row may see: its causal limit, capped by the key range.
-  const int lim = min(qpos, kend - 1);
-  // MaskT (std::true_type / std::false_type): whether the tile may need the
-  // causal / range mask.  Masked tiles (at most the last two of a
-  // workgroup) run in a loop of their own, so the mask never becomes
-  // straight-line code on the others.
-  auto compute = [&](auto MaskT, const uint16_t* kb_lds, const uint16_t* vb_lds, int k0) {
-    // S^T for the two 32-key halves of the tile (raw scores); K operands
-    // are read four steps at a time ahead of their MFMAs.
-    f32x16_t s[2];
+  // S^T of one 64-key sub-tile (raw scores, two 32-key halves); K operands
+  // are read four steps ahead of their MFMAs.
+  auto qk = [&](const uint16_t* kb_lds, f32x16_t* sv) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const uint16_t* kbase = kb_lds + 32 * kb * D;
       uint4 ka[4];
 #pragma unroll
       for (int st = 0; st < 4; ++st) ka[st] = *reinterpret_cast<const uint4*>(kbase + kx[st]);
-      s[kb] = M::run(__builtin_bit_cast(v8, ka[0]), qf[0], f32x16_t{});
+      sv[kb] = M::run(__builtin_bit_cast(v8, ka[0]), qf[0], f32x16_t{});
 #pragma unroll
       for (int st = 1; st < QSTEPS; ++st) {
         if (st + 3 < QSTEPS)
           ka[(st + 3) & 3] = *reinterpret_cast<const uint4*>(kbase + kx[st + 3]);
-        s[kb] = M::run(__builtin_bit_cast(v8, ka[st & 3]), qf[st], s[kb]);
+        sv[kb] = M::run(__builtin_bit_cast(v8, ka[st & 3]), qf[st], sv[kb]);
       }
     }
-    // Causal / range mask: slot i of half kb holds key
-    // k0 + 32 kb + 8 (i / 4) + 4 h + i % 4.
+  };
+  // Causal / range mask (MaskT = std::true_type on tiles that may need it;
+  // those run in a loop of their own so the mask is never straight-line code
+  // on the others): slot i of half kb holds key k0 + 32 kb + 8 (i/4) + 4 h + i%4.
+  const int lim = min(qpos, kend - 1);   // last key each row may see
+  auto mask = [&](auto MaskT, f32x16_t* sv, int k0) {
     if constexpr (decltype(MaskT)::value) {
       const int d = lim - k0 - 4 * h;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (32 * kb + 8 * (i >> 2) + (i & 3) > d) s[kb][i] = kNegBig;
+          if (32 * kb + 8 * (i >> 2) + (i & 3) > d) sv[kb][i] = kNegBig;
     }
-    // Online softmax in log2 units; masked scores give exp2(-huge) = 0.
+  };
+  // Online softmax in log2 units with a lazily raised maximum: the running
+  // maximum m_run moves only when a row's maximum exceeds it by more than
+  // 2^8 (or on the first tile), so probabilities stay below 256 and the O
+  // rescale is rare.  Returns the factor O must be scaled by (1 = none).
+  auto soft = [&](const f32x16_t* sv, uint32_t (*pw)[8]) {
     float mx = kNegBig;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx * scale_log2);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[kb][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+    float alpha = 1.0f;
+    if (mx > m_run + 8.0f) {
+      alpha = fast_exp2(m_run - mx);
+      m_run = mx;
+    }
     float psum = 0.0f;
-    uint32_t pw[2][8];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; i += 2) {
-        const float p0 = fast_exp2(fmaf(s[kb][i], scale_log2, -m_new));
-        const float p1 = fast_exp2(fmaf(s[kb][i + 1], scale_log2, -m_new));
+        const float p0 = fast_exp2(fmaf(sv[kb][i], scale_log2, -m_run));
+        const float p1 = fast_exp2(fmaf(sv[kb][i + 1], scale_log2, -m_run));
         psum += p0 + p1;
         pw[kb][i >> 1] = M::pack2(p0, p1);
       }
     l_run = l_run * alpha + psum;
-    if (__ballot(alpha != 1.0f)) {   // some row's max moved: rescale O (uniform branch)
+    return alpha;
+  };
+  auto rescale = [&](float alpha) {
+    if (__ballot(alpha != 1.0f)) {   // uniform branch, rare after the first tile
 #pragma unroll
       for (int b = 0; b < DBLK; ++b)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[b][i] *= alpha;
     }
-    // O^T += V^T P^T, four 16-key steps; the step's transpose reads are
-    // issued together ahead of its MFMAs.
+  };
+  // O^T += V^T P^T over one 64-key sub-tile, four 16-key steps; each step's
+  // transpose reads are issued together ahead of its MFMAs.
+  auto pv = [&](const uint16_t* vb_lds, const uint32_t (*pw)[8]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const uint32_t* pp = &pw[t >> 1][4 * (t & 1)];
@@ -797,6 +822,30 @@ __global__ __launch_bounds__(64 * W, 8 / W) void attn_chunk_mfma_kernel(
       }
     }
   };
+  // One LDS tile.  With two sub-tiles the code order lets the second
+  // half's K Q^T overlap the first half's softmax and the first half's
+  // P V overlap the second half's softmax (no branch between them).
+  auto compute = [&](auto MaskT, const uint16_t* kb_lds, const uint16_t* vb_lds, int k0) {
+    if constexpr (NSUB == 1) {
+      f32x16_t sv[2];
+      uint32_t pw[2][8];
+      qk(kb_lds, sv);
+      mask(MaskT, sv, k0);
+      rescale(soft(sv, pw));
+      pv(vb_lds, pw);
+    } else {
+      f32x16_t s0[2], s1[2];
+      uint32_t p0[2][8], p1[2][8];
+      qk(kb_lds, s0);
+      mask(MaskT, s0, k0);
+      qk(kb_lds + 64 * D, s1);
+      mask(MaskT, s1, k0 + 64);
+      rescale(soft(s0, p0));
+      pv(vb_lds, p0);
+      rescale(soft(s1, p1));
+      pv(vb_lds + 64 * D, p1);
+    }
+  };
 
   // One step: start loading the next tile into the other stage, compute
   // this one, then wait for the loads and make them visible to all.
@@ -804,9 +853,7 @@ __global__ __launch_bounds__(64 * W, 8 / W) void attn_chunk_mfma_kernel(
     const int k0 = it * KT;
     const bool more = it + 1 < ntiles;
     if (more) stage(Kn, Vn, k0 + KT);
-#pragma unroll 1
-    for (int sub = 0; sub < NSUB; ++sub)
-      compute(MaskT, Kc + 64 * sub * D, Vc + 64 * sub * D, k0 + 64 * sub);
+    compute(MaskT, Kc, Vc, k0);
     __builtin_amdgcn_s_waitcnt(0);   // this thread's LDS loads have landed
     __syncthreads();                 // ... and everyone's; the current stage is free
     if (more && k0 + 2 * KT > kend) {
@@ -1070,30 +1117,38 @@ static int dispatch(lv_dtype dt, int D, int G, int BS, const LaunchArgs& a, cons
   }
 }
 
-template <typename T, int D, int G, int W>
+template <typename T, int D, int G, int W, int BPW>
 static void launch_chunk_kernel_w(const LaunchArgs& a, const int32_t* cu, int seq_begin,
                                   int n_seqs, int max_query_len) {
   constexpr int QT = 32 * W / G;
-  const dim3 grid((max_query_len + QT - 1) / QT, a.num_kv_heads, n_seqs);
-  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16, W>), grid, dim3(64 * W), 0, a.st,
-                     (const T*)a.q, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.num_kv_heads,
-                     a.num_cache_blocks, a.bt, a.max_blocks, cu, a.ctx, seq_begin, a.scale_log2,
-                     (T*)a.out, a.out_stride);
+  const int nq = (max_query_len + QT - 1) / QT;
+  const int groups = a.num_kv_heads * n_seqs;
+  const int64_t wgs = (int64_t)((groups + kXcds - 1) / kXcds) * kXcds * nq;
+  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16, W, BPW>), dim3((unsigned)wgs),
+                     dim3(64 * W), 0, a.st, (const T*)a.q, a.q_stride, (const T*)a.kc,
+                     (const T*)a.vc, a.num_kv_heads, a.num_cache_blocks, a.bt, a.max_blocks, cu,
+                     a.ctx, seq_begin, nq, groups, a.scale_log2, (T*)a.out, a.out_stride);
 }
 
-// Wavefronts per chunk workgroup (LV_ATTN_CHUNK_WAVES = 4 or 8).
-static int chunk_waves() {
-  static const int w = env_int("LV_ATTN_CHUNK_WAVES", 4) == 8 ? 8 : 4;
-  return w;
+// Chunk workgroup shape (LV_ATTN_CHUNK_CFG): 1 = 4 wavefronts x 64-key tiles
+// (two workgroups per CU), 2 = 8 wavefronts x 128-key tiles, 3 = 4
+// wavefronts x 128-key tiles in two pipelined halves (one workgroup per CU).
+static int chunk_cfg() {
+  static const int c = [] {
+    const int v = env_int("LV_ATTN_CHUNK_CFG", 1);
+    return (v >= 1 && v <= 3) ? v : 1;
+  }();
+  return c;
 }
 
 template <typename T, int D, int G>
 static void launch_chunk_kernel(const LaunchArgs& a, const int32_t* cu, int seq_begin, int n_seqs,
                                 int max_query_len) {
-  if (chunk_waves() == 8)
-    launch_chunk_kernel_w<T, D, G, 8>(a, cu, seq_begin, n_seqs, max_query_len);
-  else
-    launch_chunk_kernel_w<T, D, G, 4>(a, cu, seq_begin, n_seqs, max_query_len);
+  switch (chunk_cfg()) {
+    case 2: launch_chunk_kernel_w<T, D, G, 8, 1>(a, cu, seq_begin, n_seqs, max_query_len); break;
+    case 3: launch_chunk_kernel_w<T, D, G, 4, 2>(a, cu, seq_begin, n_seqs, max_query_len); break;
+    default: launch_chunk_kernel_w<T, D, G, 4, 1>(a, cu, seq_begin, n_seqs, max_query_len); break;
+  }
 }
 
 template <typename T, int D>
