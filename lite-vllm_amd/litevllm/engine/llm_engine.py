@@ -13,8 +13,11 @@ sampled ids are read back, its decodes take their input ids straight from
 step k-1's device output, and the host bookkeeping of step k-1 runs while
 the GPU computes step k (a sequence that stops on EOS or a stop string thus
 computes one extra token, which is dropped; max_tokens is known ahead and
-costs nothing).  Text is produced incrementally only when somebody reads it
-(streaming, or the final output).
+costs nothing).  Text is produced only when somebody reads it: streamed
+deltas and stop strings decode only the newest tokens (incremental
+detokenization, O(1) per token instead of the reference's full decode per
+step, llm_engine.py:151-158, 213-219); a finished request's text is one full
+decode, as in the reference.
 """
 
 from __future__ import annotations
@@ -29,7 +32,7 @@ from ..cache.block_manager import BlockManager
 from ..cache.prefix_cache import PrefixCache
 from ..config import EngineConfig, SamplingParams
 from ..layers.sampler import Sampler
-from ..tokenizer import TokenizerGroup, get_tokenizer
+from ..tokenizer import IncrementalDetokenizer, TokenizerGroup, get_tokenizer
 from .model_runner import ModelRunner
 from .scheduler import Scheduler
 from .sequence import Sequence, SequenceGroup, SequenceGroupOutput, SequenceStatus
@@ -201,8 +204,13 @@ class LLMEngine:
         elif seq.data.output_len >= params.max_tokens:
             seq.status = SequenceStatus.FINISHED_LENGTH
         elif params.stop and self.tokenizer is not None:
-            text = self.tokenizer.decode(seq.data.output_token_ids, skip_special_tokens=False)
-            if any(s in text for s in params.stop):
+            d = seq.stop_detok
+            if d is None:
+                d = seq.stop_detok = IncrementalDetokenizer(skip_special_tokens=False)
+            start = max(0, len(d.text) - max(len(s) for s in params.stop) + 1)
+            d.update(self.tokenizer, seq.data.output_token_ids)
+            tail = d.text[start:]      # every match that includes new text
+            if any(s in tail for s in params.stop):
                 seq.status = SequenceStatus.FINISHED_STOPPED
 
     def _build_step_output(self, sg: SequenceGroup) -> SequenceGroupOutput:
@@ -210,8 +218,14 @@ class LLMEngine:
         finished = sg.is_finished
         text, delta = seq.emitted_text, ""
         if self.tokenizer is not None and (finished or self.stream_text):
-            text = self.tokenizer.decode(seq.data.output_token_ids,
-                                         skip_special_tokens=sg.sampling_params.skip_special_tokens)
+            skip = sg.sampling_params.skip_special_tokens
+            if finished:
+                text = self.tokenizer.decode(seq.data.output_token_ids, skip_special_tokens=skip)
+            else:
+                if seq.detok is None:
+                    seq.detok = IncrementalDetokenizer(skip_special_tokens=skip)
+                seq.detok.update(self.tokenizer, seq.data.output_token_ids)
+                text = seq.detok.text
             delta = text[len(seq.emitted_text):]
             seq.emitted_text = text
         return SequenceGroupOutput(request_id=sg.request_id, prompt_text=sg.prompt_text,

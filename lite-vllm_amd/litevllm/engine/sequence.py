@@ -5,7 +5,9 @@ per-step packing: ``Sequence.num_scheduled_tokens`` (tokens fed this step)
 and ``SequenceData.last_token`` (no prompt+output list concatenation); for
 the overlapped step loop, ``Sequence.num_inflight`` / ``inflight_row``: a
 token sampled on the device by the step in flight, not yet appended on the
-host, and its row in that step's sampled-ids tensor."""
+host, and its row in that step's sampled-ids tensor; for text,
+``detok`` (streamed output text) and ``stop_detok`` (text for stop strings,
+special tokens kept), both incremental."""
 
 from __future__ import annotations
 
@@ -13,8 +15,10 @@ import enum
 import itertools
 import time
 from dataclasses import dataclass, field
+from typing import Optional
 
 from litevllm.config import SamplingParams
+from litevllm.tokenizer.detokenizer import IncrementalDetokenizer
 
 
 class SequenceStatus(enum.Enum):
@@ -77,6 +81,8 @@ class Sequence:
     num_scheduled_tokens: int = 0  # tokens fed in the current step
     num_inflight: int = 0          # sampled on the device, not yet appended here
     inflight_row: int = -1         # row of the newest such token in its step's ids
+    detok: Optional[IncrementalDetokenizer] = None
+    stop_detok: Optional[IncrementalDetokenizer] = None
 
     @classmethod
     def create(cls, prompt_token_ids: list[int]) -> "Sequence":

@@ -1,3 +1,4 @@
+from .detokenizer import IncrementalDetokenizer
 from .tokenizer import TokenizerGroup, get_tokenizer
 
-__all__ = ["TokenizerGroup", "get_tokenizer"]
+__all__ = ["IncrementalDetokenizer", "TokenizerGroup", "get_tokenizer"]

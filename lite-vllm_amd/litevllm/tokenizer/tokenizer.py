@@ -17,6 +17,14 @@ class TokenizerGroup:
                                                   revision=revision)
         self._lock = threading.Lock()
 
+    @classmethod
+    def wrap(cls, tokenizer) -> "TokenizerGroup":
+        """A group around an already constructed Hugging Face tokenizer."""
+        g = cls.__new__(cls)
+        g._tok = tokenizer
+        g._lock = threading.Lock()
+        return g
+
     def encode(self, text: str) -> list[int]:
         with self._lock:
             return self._tok.encode(text)
