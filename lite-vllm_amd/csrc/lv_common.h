@@ -28,6 +28,10 @@ int check_launch(const char* what);
     }                                  \
   } while (0)
 
+// XCDs of an MI355X: workgroups are dispatched round-robin over them, and
+// each XCD has its own L2.
+constexpr int kXcds = 8;
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline size_t dtype_size(lv_dtype dt) { return dt == LV_F32 ? 4 : 2; }

@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "lv_common.h"
+#include "lv_mfma.h"
 
 namespace lv {
 
@@ -545,38 +546,6 @@ __global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
 // O^T keeps the query as the column, so the softmax rescale is lane-local.
 // Keys at or past the end of the needed range are zero-filled and masked.
 // ---------------------------------------------------------------------------
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef short i16x8_t __attribute__((ext_vector_type(8)));
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-template <typename T> struct Mfma32;
-template <> struct Mfma32<bf16> {
-  using v8 = bf16x8_t;
-  __device__ __forceinline__ static f32x16_t run(v8 a, v8 b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-  // Two fp32 values -> packed pair, round to nearest even (v_cvt_pk_bf16_f32).
-  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
-  }
-};
-template <> struct Mfma32<f16> {
-  using v8 = f16x8_t;
-  __device__ __forceinline__ static f32x16_t run(v8 a, v8 b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
-    return (uint32_t)float_to_f16_bits(a) | ((uint32_t)float_to_f16_bits(b) << 16);
-  }
-};
-
-constexpr int kXcds = 8;   // XCDs of an MI355X (workgroups are dispatched round-robin over them)
 
 // W wavefronts per workgroup: 32 W (query token, head) rows, and LDS tiles
 // of 16 W keys (one 16-token block staged per wavefront), computed in
@@ -595,12 +564,6 @@ template <int D, int W> struct ChunkLds {
 
 __device__ __forceinline__ i16x4_t lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)p);
-}
-
-// 16 bytes per lane from global memory straight into LDS at wave base + 16 lane.
-__device__ __forceinline__ void load_lds16(const void* g, uint16_t* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
-                                   0, 0);
 }
 
 template <typename T, int D, int G, int BS, int W, int BPW>

@@ -46,6 +46,7 @@ EXTRA_FLAGS = {
     "sampler.hip": ["-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt"],
     # products and sums rounded separately, as the reference's separate ops do
     "fused_layers.hip": ["-ffp-contract=off"],
+    "linear.hip": ["-ffp-contract=off"],
 }
 
 

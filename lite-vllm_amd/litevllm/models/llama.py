@@ -5,6 +5,7 @@ LM head is applied only to the rows that are sampled."""
 
 from __future__ import annotations
 
+import os
 from typing import Optional
 
 import torch
@@ -15,6 +16,24 @@ from litevllm.config import ModelConfig
 from litevllm.layers.attention import Attention
 from litevllm.layers.rotary_emb import RotaryEmbedding, apply_rotary_emb
 from litevllm.models.base import BaseModelForCausalLM
+
+
+# Rows up to which a projection runs on lv_linear (decode-sized batches);
+# larger batches (prefill chunks) use the library GEMM.  0 disables it.
+DECODE_GEMM_ROWS = int(os.environ.get("LV_DECODE_GEMM_ROWS", "256"))
+
+
+class Linear(nn.Linear):
+    """nn.Linear (the reference's ColumnParallelLinear / RowParallelLinear,
+    layers/linear.py:15-65) whose decode-sized calls run on the lv_linear
+    MFMA kernel; other shapes, biases and dtypes use the library GEMM."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        m = x.shape[0] if x.dim() == 2 else 0
+        if (0 < m <= DECODE_GEMM_ROWS and self.bias is None and x.is_cuda
+                and ops.linear_supported(m, self.out_features, self.in_features, x.dtype)):
+            return ops.linear(x, self.weight)
+        return super().forward(x)
 
 
 class RMSNorm(nn.Module):
@@ -44,8 +63,8 @@ class GatedMLP(nn.Module):
     def __init__(self, hidden_size: int, intermediate_size: int) -> None:
         super().__init__()
         self.intermediate_size = intermediate_size
-        self.gate_up_proj = nn.Linear(hidden_size, 2 * intermediate_size, bias=False)
-        self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+        self.gate_up_proj = Linear(hidden_size, 2 * intermediate_size, bias=False)
+        self.down_proj = Linear(intermediate_size, hidden_size, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.down_proj(ops.silu_mul(self.gate_up_proj(x)))
@@ -63,9 +82,9 @@ class DecoderAttention(nn.Module):
         self.head_dim = config.head_dim
         self.q_size = self.num_heads * self.head_dim
         self.kv_size = self.num_kv_heads * self.head_dim
-        self.qkv_proj = nn.Linear(config.hidden_size, self.q_size + 2 * self.kv_size,
-                                  bias=config.attention_bias)
-        self.o_proj = nn.Linear(self.q_size, config.hidden_size, bias=False)
+        self.qkv_proj = Linear(config.hidden_size, self.q_size + 2 * self.kv_size,
+                               bias=config.attention_bias)
+        self.o_proj = Linear(self.q_size, config.hidden_size, bias=False)
         self.use_qk_norm = use_qk_norm
         if use_qk_norm:
             self.q_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)

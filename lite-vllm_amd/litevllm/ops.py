@@ -437,3 +437,49 @@ def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch
                          _dtype_code(gate_up), _stream(dev))
     _hip.check(rc, "lv_silu_mul")
     return out
+
+
+_linear_ok: dict = {}
+
+
+def linear_supported(m: int, n: int, k: int, dtype: torch.dtype) -> bool:
+    """Whether lv_linear has a kernel for this shape (bf16/fp16, n % 32 == 0,
+    k % 128 == 0); cached per (n, k, dtype)."""
+    if dtype not in (torch.bfloat16, torch.float16) or m < 1:
+        return False
+    key = (n, k, dtype)
+    ok = _linear_ok.get(key)
+    if ok is None:
+        ok = bool(_hip.load().lv_linear_supported(m, n, k, _DTYPE_CODES[dtype]))
+        _linear_ok[key] = ok
+    return ok
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor,
+           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x @ weight.T (nn.Linear without bias) for decode-sized x ([M, K],
+    M up to a few hundred) on the MFMA kernel; raises for shapes it has no
+    kernel for (see linear_supported).
+
+    Reference: layers/linear.py:15-65 (ColumnParallelLinear /
+    RowParallelLinear = nn.Linear).
+    """
+    dev = x.device
+    for name, t in (("x", x), ("weight", weight), ("out", out)):
+        _require_device(name, t, dev)
+    M, K = x.shape
+    N = weight.shape[0]
+    _check_rows("x", x, K, x.dtype)
+    _check_rows("weight", weight, K, x.dtype)
+    if weight.shape[1] != K:
+        raise RuntimeError(f"weight {tuple(weight.shape)} does not match x {tuple(x.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=x.dtype, device=dev)
+    _check_rows("out", out, N, x.dtype)
+    if M == 0:
+        return out
+    lib = _hip.load()
+    rc = lib.lv_linear(_ptr(x), x.stride(0), _ptr(weight), weight.stride(0), _ptr(out),
+                       out.stride(0), M, N, K, _dtype_code(x), _stream(dev))
+    _hip.check(rc, "lv_linear")
+    return out
