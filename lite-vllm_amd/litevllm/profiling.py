@@ -6,6 +6,12 @@ kernels by total time, the GPU busy time against the trace span, and, for
 an engine run, the average duration of the decode-attention kernels over
 decode-only steps (a step starts at each ``pack_kernel`` dispatch; it is
 decode-only when no ``attn_chunk_mfma_kernel`` runs in it).
+
+``python -m litevllm.profiling --counters DIR`` reads the
+``*counter_collection.csv`` of a ``rocprofv3 --pmc ... --output-format csv``
+run and prints, per counter, the mean value per decode-attention launch
+pair (persistent kernel + its reduce kernel) over decode-only steps, and the
+mean per dispatch of every other kernel.
 """
 
 from __future__ import annotations
@@ -91,12 +97,82 @@ def _decode_only(rows) -> dict:
                         for k, v in acc.items()}}
 
 
+def summarize_counters(pmc_dir: str) -> str:
+    import csv
+    files = sorted(glob.glob(str(Path(pmc_dir) / "**" / "*counter_collection.csv"),
+                             recursive=True))
+    if not files:
+        raise FileNotFoundError(f"no counter_collection.csv under {pmc_dir}")
+    # dispatch id -> (kernel name, {counter: value})
+    disp: dict[int, tuple[str, dict[str, float]]] = {}
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            d = int(r.get("Dispatch_Id") or r["Correlation_Id"])
+            name, vals = disp.setdefault(d, (r["Kernel_Name"], {}))
+            vals[r["Counter_Name"]] = vals.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    order = sorted(disp)
+    counters = sorted({c for _, v in disp.values() for c in v})
+    steps, cur = [], None
+    for d in order:
+        name, vals = disp[d]
+        if "pack_kernel" in name:
+            if cur is not None:
+                steps.append(cur)
+            cur = []
+        elif cur is not None:
+            cur.append((name, vals))
+    if cur:
+        steps.append(cur)
+    pairs: list[dict[str, float]] = []
+    for st in steps:
+        if any("attn_chunk_mfma_kernel" in n for n, _ in st):
+            continue
+        acc = None
+        for n, vals in st:
+            if "attn_decode_persistent_kernel" in n:
+                if acc is not None:
+                    pairs.append(acc)
+                acc = dict(vals)
+            elif "attn_persist_reduce_kernel" in n and acc is not None:
+                for c, v in vals.items():
+                    acc[c] = acc.get(c, 0.0) + v
+        if acc is not None:
+            pairs.append(acc)
+    out = [f"dispatches with counters: {len(order)}; decode-only steps: "
+           f"{sum(1 for st in steps if not any('attn_chunk_mfma_kernel' in n for n, _ in st))}; "
+           f"decode-attention launch pairs in them: {len(pairs)}", ""]
+    if pairs:
+        out.append("| counter | mean per decode-attention launch pair (decode-only steps) |")
+        out.append("|---|---|")
+        for c in counters:
+            vals = [p[c] for p in pairs if c in p]
+            if vals:
+                out.append(f"| {c} | {statistics.mean(vals):.1f} |")
+        out.append("")
+    per: dict[str, dict[str, list[float]]] = {}
+    for d in order:
+        name, vals = disp[d]
+        for c, v in vals.items():
+            per.setdefault(_short(name, 80), {}).setdefault(c, []).append(v)
+    out.append("| kernel | counter | dispatches | mean per dispatch |")
+    out.append("|---|---|---|---|")
+    for k in sorted(per):
+        for c, v in sorted(per[k].items()):
+            out.append(f"| `{k}` | {c} | {len(v)} | {statistics.mean(v):.1f} |")
+    return "\n".join(out)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("trace_dir")
     ap.add_argument("--top", type=int, default=25)
+    ap.add_argument("--counters", action="store_true",
+                    help="trace_dir holds a rocprofv3 --pmc csv run")
     args = ap.parse_args()
-    print(summarize(args.trace_dir, args.top))
+    if args.counters:
+        print(summarize_counters(args.trace_dir))
+    else:
+        print(summarize(args.trace_dir, args.top))
 
 
 if __name__ == "__main__":
