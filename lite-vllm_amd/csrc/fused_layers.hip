@@ -23,31 +23,42 @@ namespace lv {
 constexpr int kFusedThreads = 256;
 
 // ---------------------------------------------------------------------------
-// add_rms_norm: one wavefront per token row; the row stays in registers
-// (NC chunks of 16 bytes per lane).
+// add_rms_norm: one single-wavefront workgroup per token row (rows spread
+// over all CUs); the row stays in registers (NC chunks of 16 bytes per lane).
 // ---------------------------------------------------------------------------
 template <typename T, int NC>
-__global__ __launch_bounds__(kFusedThreads) void add_rms_norm_kernel(
+__global__ __launch_bounds__(64) void add_rms_norm_kernel(
     const T* __restrict__ x, int64_t x_stride, T* __restrict__ residual, int64_t res_stride,
     const T* __restrict__ weight, T* __restrict__ out, int64_t out_stride, int64_t num_tokens,
     int hidden, float eps) {
   constexpr int P = elem<T>::kPer16B;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * (kFusedThreads / 64) + (threadIdx.x >> 6);
-  if (row >= num_tokens) return;
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
   const int chunks = hidden / P;
   const T* xr = x + row * x_stride;
   T* rr = residual ? residual + row * res_stride : nullptr;
+  // every load of the row is issued before the first use: one memory round
+  // trip, then the reduction
+  uint4 xv[NC], rv[NC], wv[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      xv[j] = load16(xr + c * P);
+      if (rr) rv[j] = load16(rr + c * P);
+      wv[j] = load16(weight + c * P);
+    }
+  }
   float v[NC][P];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
     const int c = lane + 64 * j;
     if (c < chunks) {
-      elem<T>::unpack(load16(xr + c * P), v[j]);
+      elem<T>::unpack(xv[j], v[j]);
       if (rr) {
         float r[P];
-        elem<T>::unpack(load16(rr + c * P), r);
+        elem<T>::unpack(rv[j], r);
 #pragma unroll
         for (int i = 0; i < P; ++i) v[j][i] = round_to<T>(v[j][i] + r[i]);
         store16(rr + c * P, pack16<T>(v[j]));
@@ -64,7 +75,7 @@ __global__ __launch_bounds__(kFusedThreads) void add_rms_norm_kernel(
     const int c = lane + 64 * j;
     if (c < chunks) {
       float w[P], o[P];
-      elem<T>::unpack(load16(weight + c * P), w);
+      elem<T>::unpack(wv[j], w);
 #pragma unroll
       for (int i = 0; i < P; ++i) o[i] = round_to<T>(w[i] * round_to<T>(v[j][i] * inv));
       store16(orow + c * P, pack16<T>(o));
@@ -97,9 +108,13 @@ __global__ __launch_bounds__(kFusedThreads) void qk_norm_rope_cache_kernel(
   if (t >= num_tokens) return;  // whole groups leave together (W divides 64)
   const int hs = (int)(gid - t * slots_per_token);
   const T* src = qkv + t * qkv_stride + (int64_t)hs * D;
+  // the position and slot loads go first: cos/sin depend on the position,
+  // and everything else is independent, so the kernel takes two memory
+  // round trips (row, weights, position, slot; then cos/sin)
+  const int64_t pos = positions[t];
+  const int64_t slot = slots[t];
 
   if (hs >= num_heads + num_kv_heads) {  // value head: plain copy into the cache
-    const int64_t slot = slots[t];
     if (slot < 0 || slot >= num_slots) return;
     T* dst = value_cache + slot * ((int64_t)num_kv_heads * D) +
              (int64_t)(hs - num_heads - num_kv_heads) * D;
@@ -113,14 +128,26 @@ __global__ __launch_bounds__(kFusedThreads) void qk_norm_rope_cache_kernel(
   }
 
   const bool is_q = hs < num_heads;
-  float x1[PPL], x2[PPL];
+  if (!is_q && (slot < 0 || slot >= num_slots)) return;
+  const T* nw = is_q ? q_norm_w : k_norm_w;
+  float x1[PPL], x2[PPL], w1[PPL], w2[PPL];
 #pragma unroll
   for (int p = 0; p < PPL; ++p) {
     const int i = lane_in_group + W * p;
     x1[p] = elem<T>::load(src + i);
     x2[p] = elem<T>::load(src + i + HALF);
+    w1[p] = nw ? elem<T>::load(nw + i) : 0.f;
+    w2[p] = nw ? elem<T>::load(nw + i + HALF) : 0.f;
   }
-  const T* nw = is_q ? q_norm_w : k_norm_w;
+  // an out-of-range position has no cos/sin row: the output becomes NaN
+  const bool pos_ok = pos >= 0 && pos < max_position;
+  float cs[PPL], sn[PPL];
+#pragma unroll
+  for (int p = 0; p < PPL; ++p) {
+    const int i = lane_in_group + W * p;
+    cs[p] = pos_ok ? elem<T>::load(cos_cache + pos * HALF + i) : __builtin_nanf("");
+    sn[p] = pos_ok ? elem<T>::load(sin_cache + pos * HALF + i) : __builtin_nanf("");
+  }
   if (nw) {
     float ss = 0.f;
 #pragma unroll
@@ -129,29 +156,17 @@ __global__ __launch_bounds__(kFusedThreads) void qk_norm_rope_cache_kernel(
     const float inv = rsqrtf(ss / (float)D + eps);
 #pragma unroll
     for (int p = 0; p < PPL; ++p) {
-      const int i = lane_in_group + W * p;
-      x1[p] = round_to<T>(elem<T>::load(nw + i) * round_to<T>(x1[p] * inv));
-      x2[p] = round_to<T>(elem<T>::load(nw + i + HALF) * round_to<T>(x2[p] * inv));
+      x1[p] = round_to<T>(w1[p] * round_to<T>(x1[p] * inv));
+      x2[p] = round_to<T>(w2[p] * round_to<T>(x2[p] * inv));
     }
   }
-  const int64_t pos = positions[t];
-  const bool pos_ok = pos >= 0 && pos < max_position;
-  T* dst;
-  if (is_q) {
-    dst = q_out + t * q_out_stride + (int64_t)hs * D;
-  } else {
-    const int64_t slot = slots[t];
-    if (slot < 0 || slot >= num_slots) return;
-    dst = key_cache + slot * ((int64_t)num_kv_heads * D) + (int64_t)(hs - num_heads) * D;
-  }
+  T* dst = is_q ? q_out + t * q_out_stride + (int64_t)hs * D
+                : key_cache + slot * ((int64_t)num_kv_heads * D) + (int64_t)(hs - num_heads) * D;
 #pragma unroll
   for (int p = 0; p < PPL; ++p) {
     const int i = lane_in_group + W * p;
-    // an out-of-range position has no cos/sin row: the output becomes NaN
-    const float c = pos_ok ? elem<T>::load(cos_cache + pos * HALF + i) : __builtin_nanf("");
-    const float s = pos_ok ? elem<T>::load(sin_cache + pos * HALF + i) : __builtin_nanf("");
-    const float o1 = round_to<T>(round_to<T>(x1[p] * c) - round_to<T>(x2[p] * s));
-    const float o2 = round_to<T>(round_to<T>(x2[p] * c) + round_to<T>(x1[p] * s));
+    const float o1 = round_to<T>(round_to<T>(x1[p] * cs[p]) - round_to<T>(x2[p] * sn[p]));
+    const float o2 = round_to<T>(round_to<T>(x2[p] * cs[p]) + round_to<T>(x1[p] * sn[p]));
     elem<T>::store(dst + i, o1);
     elem<T>::store(dst + i + HALF, o2);
   }
@@ -193,15 +208,15 @@ int launch_add_rms_norm(const void* x, int64_t xs, void* res, int64_t rs, const 
   constexpr int P = elem<T>::kPer16B;
   const int chunks = hidden / P;
   const int nc = (chunks + 63) / 64;
-  const dim3 grid((unsigned)((n + 3) / 4));
+  const dim3 grid((unsigned)n);
   const T* xp = static_cast<const T*>(x);
   T* rp = static_cast<T*>(res);
   const T* wp = static_cast<const T*>(w);
   T* op = static_cast<T*>(out);
 #define LV_RMS_CASE(NCV)                                                                     \
   if (nc <= NCV) {                                                                           \
-    add_rms_norm_kernel<T, NCV><<<grid, kFusedThreads, 0, st>>>(xp, xs, rp, rs, wp, op, os, n, \
-                                                                hidden, eps);                \
+    add_rms_norm_kernel<T, NCV><<<grid, 64, 0, st>>>(xp, xs, rp, rs, wp, op, os, n, hidden,    \
+                                                     eps);                                   \
     return check_launch("add_rms_norm_kernel");                                              \
   }
   LV_RMS_CASE(1)
