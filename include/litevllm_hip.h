@@ -51,7 +51,7 @@ const char* lv_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int lv_abi_version(void);
-#define LV_ABI_VERSION 3
+#define LV_ABI_VERSION 4
 
 /* ------------------------------------------------------------------------
  * (1) Ragged-batch packing.
@@ -269,19 +269,31 @@ int lv_silu_mul(const void* gate_up_dev, int64_t in_stride_t, void* out_dev,
  * Replaces nn.Linear without bias -- ColumnParallelLinear /
  * RowParallelLinear (reference litevllm/layers/linear.py:15-65) as used for
  * the q/k/v, o, gate/up and down projections (models/qwen3.py:45-48,
- * models/llama.py:33-35, 58-61) of decode steps:
- *   y[m, n] = to_dtype(sum_k x[m, k] * weight[n, k])     (fp32 accumulation)
- * weight is [N, K] with row stride weight_stride_n; x [M, K] and y [M, N]
- * with row strides in elements; x/weight rows 16-byte aligned, y rows 8-byte
- * aligned.  bf16/fp16 with N % 32 == 0 and K % 128 == 0 have a kernel
- * (lv_linear_supported); anything else returns LV_ERR_UNSUPPORTED and the
- * caller uses a library GEMM.  Meant for M up to a few hundred; larger M
- * belong to the library GEMM. */
-int lv_linear_supported(int64_t m, int64_t n, int64_t k, lv_dtype dtype);
+ * models/llama.py:33-35, 58-61) of decode steps -- and, with
+ * LV_ACT_SILU_MUL, the gated-MLP input of down_proj
+ * F.silu(gate_proj(x)) * up_proj(x) (llama.py:38):
+ *   LV_ACT_NONE      y[m, n] = to_dtype(sum_k x[m, k] * weight[n, k])
+ *   LV_ACT_SILU_MUL  g, u = the same sums with weight rows n and N + n;
+ *                    y[m, n] = to_dtype(to_dtype(silu(to_dtype(g))) * to_dtype(u))
+ * fp32 accumulation; the k order of the sums is the same for both forms, so
+ * the silu_mul form equals lv_silu_mul applied to the plain form's output
+ * over the [2N, K] weight.  weight is [N, K] ([2N, K] for LV_ACT_SILU_MUL)
+ * with row stride weight_stride_n; x [M, K] and y [M, N] with row strides in
+ * elements; x/weight rows 16-byte aligned, y rows 8-byte aligned.  bf16/fp16
+ * with N % 32 == 0 and K % 128 == 0 have a kernel (lv_linear_supported);
+ * anything else returns LV_ERR_UNSUPPORTED and the caller uses a library
+ * GEMM.  Meant for M up to a few hundred; larger M belong to the library
+ * GEMM. */
+typedef enum lv_activation {
+  LV_ACT_NONE = 0,
+  LV_ACT_SILU_MUL = 1
+} lv_activation;
+
+int lv_linear_supported(int64_t m, int64_t n, int64_t k, int32_t activation, lv_dtype dtype);
 
 int lv_linear(const void* x_dev, int64_t x_stride_t, const void* weight_dev,
               int64_t weight_stride_n, void* y_dev, int64_t y_stride_t, int64_t m, int64_t n,
-              int64_t k, lv_dtype dtype, void* stream);
+              int64_t k, int32_t activation, lv_dtype dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,8 @@ LIB_NAME = "liblitevllm_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 LV_F32, LV_F16, LV_BF16 = 0, 1, 2
-ABI_VERSION = 3
+LV_ACT_NONE, LV_ACT_SILU_MUL = 0, 1
+ABI_VERSION = 4
 
 # Every symbol the header declares, with (restype, argtypes).
 _c_i32, _c_i64, _c_f32, _c_p, _c_sz = (
@@ -86,12 +87,12 @@ SIGNATURES: dict[str, tuple] = {
         _c_i64, _c_i32,                # num_tokens, intermediate
         ctypes.c_int, _c_p,            # dtype, stream
     ]),
-    "lv_linear_supported": (ctypes.c_int, [_c_i64, _c_i64, _c_i64, ctypes.c_int]),
+    "lv_linear_supported": (ctypes.c_int, [_c_i64, _c_i64, _c_i64, _c_i32, ctypes.c_int]),
     "lv_linear": (ctypes.c_int, [
         _c_p, _c_i64, _c_p, _c_i64,    # x, x_stride, weight, weight_stride
         _c_p, _c_i64,                  # y, y_stride
         _c_i64, _c_i64, _c_i64,        # m, n, k
-        ctypes.c_int, _c_p,            # dtype, stream
+        _c_i32, ctypes.c_int, _c_p,    # activation, dtype, stream
     ]),
 }
 

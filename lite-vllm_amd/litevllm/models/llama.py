@@ -67,6 +67,12 @@ class GatedMLP(nn.Module):
         self.down_proj = Linear(intermediate_size, hidden_size, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        m = x.shape[0] if x.dim() == 2 else 0
+        if (0 < m <= DECODE_GEMM_ROWS and x.is_cuda and self.gate_up_proj.bias is None
+                and ops.linear_supported(m, self.intermediate_size,
+                                         self.gate_up_proj.in_features, x.dtype, "silu_mul")):
+            # decode-sized: gate|up projection with SiLU * up in its epilogue
+            return self.down_proj(ops.linear(x, self.gate_up_proj.weight, activation="silu_mul"))
         return self.down_proj(ops.silu_mul(self.gate_up_proj(x)))
 
 

@@ -439,39 +439,46 @@ def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch
     return out
 
 
+_ACTIVATIONS = {None: _hip.LV_ACT_NONE, "silu_mul": _hip.LV_ACT_SILU_MUL}
 _linear_ok: dict = {}
 
 
-def linear_supported(m: int, n: int, k: int, dtype: torch.dtype) -> bool:
+def linear_supported(m: int, n: int, k: int, dtype: torch.dtype,
+                     activation: Optional[str] = None) -> bool:
     """Whether lv_linear has a kernel for this shape (bf16/fp16, n % 32 == 0,
-    k % 128 == 0); cached per (n, k, dtype)."""
+    k % 128 == 0; n is the output width); cached per (n, k, dtype,
+    activation)."""
     if dtype not in (torch.bfloat16, torch.float16) or m < 1:
         return False
-    key = (n, k, dtype)
+    key = (n, k, dtype, activation)
     ok = _linear_ok.get(key)
     if ok is None:
-        ok = bool(_hip.load().lv_linear_supported(m, n, k, _DTYPE_CODES[dtype]))
+        ok = bool(_hip.load().lv_linear_supported(m, n, k, _ACTIVATIONS[activation],
+                                                  _DTYPE_CODES[dtype]))
         _linear_ok[key] = ok
     return ok
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor,
+def linear(x: torch.Tensor, weight: torch.Tensor, activation: Optional[str] = None,
            out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y = x @ weight.T (nn.Linear without bias) for decode-sized x ([M, K],
-    M up to a few hundred) on the MFMA kernel; raises for shapes it has no
-    kernel for (see linear_supported).
+    M up to a few hundred) on the MFMA kernel; with activation="silu_mul" and
+    weight = [gate; up] ([2N, K]): y = silu_mul(x @ weight.T), the same
+    values lv_silu_mul gives on the plain product.  Raises for shapes it has
+    no kernel for (see linear_supported).
 
     Reference: layers/linear.py:15-65 (ColumnParallelLinear /
-    RowParallelLinear = nn.Linear).
+    RowParallelLinear = nn.Linear), models/llama.py:38.
     """
     dev = x.device
     for name, t in (("x", x), ("weight", weight), ("out", out)):
         _require_device(name, t, dev)
     M, K = x.shape
-    N = weight.shape[0]
+    rows = weight.shape[0]
+    N = rows // 2 if activation == "silu_mul" else rows
     _check_rows("x", x, K, x.dtype)
     _check_rows("weight", weight, K, x.dtype)
-    if weight.shape[1] != K:
+    if weight.shape[1] != K or (activation == "silu_mul" and rows % 2):
         raise RuntimeError(f"weight {tuple(weight.shape)} does not match x {tuple(x.shape)}")
     if out is None:
         out = torch.empty((M, N), dtype=x.dtype, device=dev)
@@ -480,6 +487,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor,
         return out
     lib = _hip.load()
     rc = lib.lv_linear(_ptr(x), x.stride(0), _ptr(weight), weight.stride(0), _ptr(out),
-                       out.stride(0), M, N, K, _dtype_code(x), _stream(dev))
+                       out.stride(0), M, N, K, _ACTIVATIONS[activation], _dtype_code(x),
+                       _stream(dev))
     _hip.check(rc, "lv_linear")
     return out

@@ -84,9 +84,36 @@ def test_strided_rows_and_out_buffer():
 
 def test_unsupported_shapes_raise_and_report():
     assert not ops.linear_supported(8, 100, 1024, torch.bfloat16)   # n % 32
+    assert not ops.linear_supported(8, 100, 1024, torch.bfloat16, "silu_mul")
     assert not ops.linear_supported(8, 1024, 1000, torch.bfloat16)  # k % 128
     assert not ops.linear_supported(8, 1024, 1024, torch.float32)
     x = torch.randn(8, 1000, device="cuda").to(torch.bfloat16)
     w = torch.randn(1024, 1000, device="cuda").to(torch.bfloat16)
     with pytest.raises(RuntimeError, match="no kernel"):
         ops.linear(x, w)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [1, 64, 200, 256])
+@pytest.mark.parametrize("cfg", ["0", "1"])
+def test_silu_mul_epilogue_equals_plain_then_silu_mul(dtype, m, cfg, monkeypatch):
+    """The fused gate|up + SiLU form gives exactly lv_silu_mul of the plain
+    product (same k order of the sums), and is within rounding of the fp32
+    composition silu(x g^T) * (x u^T)."""
+    inter, k = 3072, 1024
+    g = torch.Generator(device="cuda").manual_seed(m + 11)
+    x = torch.randn(m, k, device="cuda", generator=g).to(dtype)
+    w = (torch.randn(2 * inter, k, device="cuda", generator=g) * k ** -0.5).to(dtype)
+    assert ops.linear_supported(m, inter, k, dtype, "silu_mul")
+    monkeypatch.setenv("LV_LINEAR_SILU_CFG", cfg)
+    fused = ops.linear(x, w, activation="silu_mul")
+    monkeypatch.delenv("LV_LINEAR_SILU_CFG")
+    plain = ops.linear(x, w)
+    assert torch.equal(fused, ops.silu_mul(plain))
+    ref = x.float() @ w.float().T
+    gate, up = ref[:, :inter], ref[:, inter:]
+    want = torch.nn.functional.silu(gate) * up
+    err = (fused.float() - want).abs()
+    tol = (4 * _ulp(want, dtype) + 4 * _ulp(up, dtype) * (gate.abs() + 1)
+           + 2 * _ulp(gate, dtype) * up.abs() + 1e-5)
+    assert (err <= tol).all(), err.max()
