@@ -278,9 +278,15 @@ def bench_e2e(args):
     orig_accepts = mr.DecodeGraphs.accepts
 
     def step_bytes(meta):
+        """K/V rows each read once per row -- a block that the step's
+        shared-prefix pass reads once for a group counts once -- plus q,
+        out, table entries, context lengths, and the prefix pass's fp32
+        partials (written, then read by the merge)."""
         B = meta.num_decodes
-        return (meta.num_context_tokens * hkv * D * 2 * 2 + 2 * B * H * D * 2
-                + meta.num_context_blocks * 4 + B * 4)
+        kv_tokens = meta.num_context_tokens - meta.prefix_saved_blocks * 16
+        return (kv_tokens * hkv * D * 2 * 2 + 2 * B * H * D * 2
+                + meta.num_context_blocks * 4 + B * 4
+                + meta.prefix_partial_rows * H * (D + 2) * 4 * 2)
 
     def exec_probe(self, meta):
         probe["meta"] = meta
@@ -365,7 +371,8 @@ def bench_e2e(args):
             "num_seqs": len(prompts), "prompt_tokens": sum(map(len, prompts)),
             "output_tokens": n_out, "prefix_hit_tokens": eng.prefix_cache.hit_tokens - hits0,
             "num_gpu_blocks": eng.config.cache_config.num_gpu_blocks,
-            "kernel": "lv_paged_attention decode (attn_decode_persistent_kernel + "
+            "kernel": "lv_paged_attention_prefix decode (shared-prefix pass "
+                      "attn_chunk_mfma_kernel<PFX> + attn_decode_persistent_kernel + "
                       "attn_persist_reduce_kernel), decode-only steps",
             "decode_graphs": not args.eager,
             "roofline_sample": ("every decode-only step" if args.eager else

@@ -51,7 +51,7 @@ const char* lv_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int lv_abi_version(void);
-#define LV_ABI_VERSION 4
+#define LV_ABI_VERSION 5
 
 /* ------------------------------------------------------------------------
  * (1) Ragged-batch packing.
@@ -180,6 +180,61 @@ int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
                        void* out_dev, int64_t out_stride_t,
                        void* workspace_dev, size_t workspace_bytes,
                        lv_dtype dtype, void* stream);
+
+/* Shared-prefix (cascade) variant of lv_paged_attention for the decode rows.
+ *
+ * Replaces the same reference code as lv_paged_attention (attention.py:
+ * 91-139); the reference has no shared-prefix pass: every decode row reads
+ * its whole context.  Here decode rows whose block tables start with the
+ * same physical blocks (a prefix-cache hit on a common prompt) form a group;
+ * the group's prefix keys are read once for all its members (MFMA kernel,
+ * members as the query rows), each row's remaining blocks are walked as in
+ * lv_paged_attention, and the two softmax partials are merged.  Results
+ * equal lv_paged_attention's to fp32 rounding.
+ *
+ * prefix_blocks: int32 [num_decodes], leading blocks of row i attended by
+ * the prefix pass (0 = none); for a member of a group it is the group's
+ * prefix length, at most 128 blocks, and prefix_blocks[i] * block_size <=
+ * context_lens[i].  prefix_members: int32, the member rows of each group
+ * listed together.  prefix_items: int32 [max_items][4], 16-byte aligned,
+ * (may be NULL when max_items is 0),
+ * one work item per (group, slice of up to 128 / G members, 128-key split
+ * of the prefix): {leader row, index of the slice's first member in
+ * prefix_members, members in the slice, split}; leader row < 0 marks an
+ * unused item.  Every member's prefix rows must be covered by exactly one
+ * item per split, and the first prefix_blocks[leader] entries of every
+ * member's block table must equal the leader's (the pass reads the leader's
+ * table).  A slice holds at most 128 / G members (more are not read).
+ * Leader and member rows outside [0, num_decodes) and splits outside
+ * [0, 16) are skipped; every index an item names into prefix_members must
+ * lie inside it.
+ * prefix_workspace: at least lv_paged_attention_prefix_workspace_size(...)
+ * bytes, 256-B aligned, contents need not be initialised; one per stream.
+ * Supported: bf16 / fp16, head_dim 64 / 128, block_size 16, G in
+ * {1, 2, 4, 8}, at most 8 kv heads, 1 <= num_decodes <= 7000 (else
+ * LV_ERR_UNSUPPORTED).  Prefill-chunk rows (num_decodes < num_seqs) are
+ * handled exactly as by lv_paged_attention.
+ */
+size_t lv_paged_attention_prefix_workspace_size(int32_t num_decodes, int32_t num_heads,
+                                                int32_t head_dim);
+
+int lv_paged_attention_prefix(const void* query_dev, int64_t q_stride_t,
+                              const void* key_cache_dev, const void* value_cache_dev,
+                              int64_t num_cache_blocks,
+                              const int32_t* block_tables_dev, int32_t max_blocks,
+                              const int32_t* cu_seqlens_dev,
+                              const int32_t* context_lens_dev,
+                              int32_t num_seqs, int32_t num_decodes, int64_t num_tokens,
+                              int32_t max_query_len,
+                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              int32_t block_size, float scale,
+                              void* out_dev, int64_t out_stride_t,
+                              void* workspace_dev, size_t workspace_bytes,
+                              const int32_t* prefix_blocks_dev,
+                              const int32_t* prefix_items_dev, int32_t max_items,
+                              const int32_t* prefix_members_dev,
+                              void* prefix_workspace_dev, size_t prefix_workspace_bytes,
+                              lv_dtype dtype, void* stream);
 
 /* ------------------------------------------------------------------------
  * (4) Fused greedy / temperature sampler.

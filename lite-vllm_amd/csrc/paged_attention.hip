@@ -315,19 +315,54 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(
 // orders the partial writes before their reads without any device-scope
 // fence inside the streaming kernel).
 // ---------------------------------------------------------------------------
+// Shared-prefix (cascade) pass.  Decode sequences whose block tables begin
+// with the same physical blocks (prefix-cache hits) form a group; the
+// group's first P blocks are attended once for all members by the MFMA
+// kernel in prefix mode, and the decode kernel only walks each member's
+// remaining blocks and merges the prefix partials in.  Prefix partials are
+// indexed [row][query head][split] (split = 128-key slice of the prefix) and
+// hold (m, l) in log2 units and acc normalised by l.
+struct PrefixArgs {
+  const int32_t* blocks;   // [num_decodes] leading blocks handled by the prefix pass (0 = none)
+  const int32_t* items;    // [max_items][4]: leader row, first member, member count, split
+  const int32_t* members;  // member rows, grouped
+  int max_items;
+  float* ml;               // [rows][H][kPrefixMaxSplits][2]
+  float* acc;              // [rows][H][kPrefixMaxSplits][D]
+};
+constexpr int kPrefixKeysPerSplit = 128;
+constexpr int kPrefixMaxSplits = 16;   // prefixes up to 2048 tokens
+constexpr int kPrefixMaxBlocks = kPrefixKeysPerSplit * kPrefixMaxSplits / 16;
+constexpr int kPrefixMaxRows = 7000;   // decode rows: offsets + skips stay in 56 KB of LDS
+
 constexpr int kPersistMaxWaves = 8;  // kv heads per workgroup (one wavefront each)
 constexpr int kPersistMaxSeqs = 15000;  // (B+1) ints of LDS stay under 60 KB
 
 // Exclusive scan of ceil(min(ctx, max_tokens) / bs) into s_off[0..n] by one
 // workgroup (integer, order-independent).
+// With a shared-prefix pass, sequence i's first skip(i) blocks are attended
+// there and left out here.
 template <int BS>
-__device__ void scan_block_counts(const int32_t* __restrict__ ctx, int n, int max_tokens,
-                                  int32_t* s_off, int32_t* s_part) {
+__device__ __forceinline__ int walked_blocks(const int32_t* __restrict__ ctx,
+                                            const int32_t* __restrict__ skip, int i,
+                                            int max_tokens) {
+  const int nb = (min(max(ctx[i], 0), max_tokens) + BS - 1) / BS;
+  return skip ? nb - min(max(skip[i], 0), min(nb, kPrefixMaxBlocks)) : nb;
+}
+
+template <int BS>
+__device__ void scan_block_counts(const int32_t* __restrict__ ctx,
+                                  const int32_t* __restrict__ skip, int n, int max_tokens,
+                                  int32_t* s_off, int32_t* s_part, int32_t* s_skip) {
   const int t = threadIdx.x, nt = blockDim.x;
   const int per = (n + nt - 1) / nt;
   const int lo = min(n, t * per), hi = min(n, lo + per);
   int32_t sum = 0;
-  for (int i = lo; i < hi; ++i) sum += (min(max(ctx[i], 0), max_tokens) + BS - 1) / BS;
+  for (int i = lo; i < hi; ++i) {
+    const int w = walked_blocks<BS>(ctx, skip, i, max_tokens);
+    if (skip) s_skip[i] = (min(max(ctx[i], 0), max_tokens) + BS - 1) / BS - w;
+    sum += w;
+  }
   s_part[t] = sum;
   __syncthreads();
   for (int d = 1; d < nt; d <<= 1) {
@@ -339,7 +374,7 @@ __device__ void scan_block_counts(const int32_t* __restrict__ ctx, int n, int ma
   int32_t run = (t == 0) ? 0 : s_part[t - 1];
   for (int i = lo; i < hi; ++i) {
     s_off[i] = run;
-    run += (min(max(ctx[i], 0), max_tokens) + BS - 1) / BS;
+    run += walked_blocks<BS>(ctx, skip, i, max_tokens);
   }
   if (t == nt - 1) s_off[n] = s_part[nt - 1];
   __syncthreads();
@@ -351,17 +386,25 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
     const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
     const int32_t* __restrict__ block_tables, int max_blocks, const int32_t* __restrict__ ctx,
     int num_seqs, float scale_log2, T* __restrict__ out, int64_t out_stride,
-    int32_t* __restrict__ ws_off, float* __restrict__ ws_acc, float* __restrict__ ws_ml) {
+    int32_t* __restrict__ ws_off, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
+    PrefixArgs pfx) {
   using S = HeadState<T, D, G, BS, NT>;
   constexpr int VEC = S::VEC;
-  extern __shared__ int32_t s_off[];               // num_seqs + 1
+  // LDS: s_off [num_seqs + 1], then (shared-prefix pass only) s_skip [num_seqs]
+  extern __shared__ int32_t s_off[];
+  int32_t* s_skip = s_off + num_seqs + 1;
   __shared__ int32_t s_part[kPersistMaxWaves * 64];
   const int max_tokens = max_blocks * BS;
-  scan_block_counts<BS>(ctx, num_seqs, max_tokens, s_off, s_part);
+  const bool has_pfx = pfx.blocks != nullptr;
+  scan_block_counts<BS>(ctx, pfx.blocks, num_seqs, max_tokens, s_off, s_part, s_skip);
   const int total = s_off[num_seqs];
   const int H = num_kv_heads * G;
+  // ws_off: offsets [num_seqs + 1], then each sequence's skipped blocks
   if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i <= num_seqs; i += blockDim.x) ws_off[i] = s_off[i];
+    for (int i = threadIdx.x; i <= num_seqs; i += blockDim.x) {
+      ws_off[i] = s_off[i];
+      if (has_pfx && i < num_seqs) ws_off[num_seqs + 1 + i] = s_skip[i];
+    }
   if (total == 0) return;
   const int per = (total + gridDim.x - 1) / gridDim.x;
   const int r0 = blockIdx.x * per;
@@ -383,14 +426,43 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
 
   int cur = -1;     // sequence whose state st holds (uniform)
   int cur_end = 0;  // its context length
+  int cur_skip = 0; // its leading blocks attended by the shared-prefix pass
 
   // Finish sequence sq: a piece covering the whole sequence goes straight to
   // `out`, any other piece to this workgroup's slot 0 (first piece) or 1.
-  auto finish = [&](int sq) {
+  auto finish = [&](int sq) __attribute__((always_inline)) {
     st.merge_token_groups();
     const int a = s_off[sq], b = s_off[sq + 1];
     const bool whole = a >= r0 && b <= r1;
     if (st.tg != 0) return;
+    if (whole && cur_skip > 0) {
+      // fold in the prefix partials (splits of 128 keys), then normalise
+      const int nsplit = (cur_skip * BS + kPrefixKeysPerSplit - 1) / kPrefixKeysPerSplit;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const int hq = kvh * G + g;
+        const int64_t pb = ((int64_t)sq * H + hq) * kPrefixMaxSplits;
+        float mx = st.m[g];
+        for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, pfx.ml[(pb + sp) * 2]);
+        const float fs = fast_exp2(st.m[g] - mx);
+        float L = st.l[g] * fs;
+        float o[S::VEC];
+#pragma unroll
+        for (int j = 0; j < S::VEC; ++j) o[j] = st.acc[g][j] * fs;
+        for (int sp = 0; sp < nsplit; ++sp) {
+          const float f = pfx.ml[(pb + sp) * 2 + 1] * fast_exp2(pfx.ml[(pb + sp) * 2] - mx);
+          L += f;
+          const float* ap = pfx.acc + (pb + sp) * D + st.dc * VEC;
+#pragma unroll
+          for (int j = 0; j < S::VEC; ++j) o[j] = fmaf(ap[j], f, o[j]);
+        }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + st.dc * VEC;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, o[j] * inv);
+      }
+      return;
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int hq = kvh * G + g;
@@ -427,7 +499,7 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
         if (s_off[mid] <= j) lo = mid; else hi = mid - 1;
       }
       lseq = lo;
-      lblk = j - s_off[lo];
+      lblk = j - s_off[lo] + (has_pfx ? s_skip[lo] : 0);   // block index in the table
       id = block_tables[(int64_t)lo * max_blocks + lblk];
     }
     if (id < 0 || id >= num_cache_blocks) id = 0;
@@ -442,6 +514,7 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
         if (cur >= 0) finish(cur);
         cur = sq;
         cur_end = min(max(ctx[sq], 0), max_tokens);
+        cur_skip = has_pfx ? s_skip[sq] : 0;
         st.init(q + (int64_t)sq * q_stride + (int64_t)kvh * G * D, scale_log2, lane);
       }
       st.process(kk, vv, lb, real ? cur_end : -1);
@@ -489,25 +562,34 @@ template <typename T, int D>
 __global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
     const int32_t* __restrict__ ws_off, int num_seqs, int num_wgs, int num_heads,
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
-    T* __restrict__ out, int64_t out_stride) {
+    T* __restrict__ out, int64_t out_stride, PrefixArgs pfx, int block_size) {
   const int sq = blockIdx.x;
   const int hq = blockIdx.y;
   const int d = threadIdx.x;
   const int total = ws_off[num_seqs];
   const int a = ws_off[sq], b = ws_off[sq + 1];
   T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + d;
-  if (a == b) {
+  // blocks of this sequence attended by the shared-prefix pass, and its splits
+  const int skip = pfx.blocks ? ws_off[num_seqs + 1 + sq] : 0;
+  const int nsplit = (skip * block_size + kPrefixKeysPerSplit - 1) / kPrefixKeysPerSplit;
+  const int64_t pb = ((int64_t)sq * num_heads + hq) * kPrefixMaxSplits;
+  int g0 = 0, g1 = -1;    // ranges holding pieces of the walked blocks
+  if (a != b) {
+    const int per = (total + num_wgs - 1) / num_wgs;
+    g0 = a / per;
+    g1 = (b - 1) / per;
+    if (g0 == g1) return;   // finished (with its prefix) by the decode kernel
+  } else if (nsplit == 0) {
     elem<T>::store(op, 0.0f);
     return;
   }
-  const int per = (total + num_wgs - 1) / num_wgs;
-  const int g0 = a / per, g1 = (b - 1) / per;
-  if (g0 == g1) return;
+  const int per = a != b ? (total + num_wgs - 1) / num_wgs : 1;
   float M = kNegBig;
   for (int g = g0; g <= g1; ++g) {
     const int slot = (a <= g * per) ? 0 : 1;
     M = fmaxf(M, ws_ml[(((int64_t)g * 2 + slot) * num_heads + hq) * 2]);
   }
+  for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, pfx.ml[(pb + sp) * 2]);
   float L = 0.0f, O = 0.0f;
   for (int g = g0; g <= g1; ++g) {
     const int slot = (a <= g * per) ? 0 : 1;
@@ -515,6 +597,11 @@ __global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
     const float f = ws_ml[base * 2 + 1] * fast_exp2(ws_ml[base * 2] - M);
     L += f;
     O = fmaf(ws_acc[base * D + d], f, O);
+  }
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float f = pfx.ml[(pb + sp) * 2 + 1] * fast_exp2(pfx.ml[(pb + sp) * 2] - M);
+    L += f;
+    O = fmaf(pfx.acc[(pb + sp) * D + d], f, O);
   }
   elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
 }
@@ -562,17 +649,24 @@ template <int D, int W> struct ChunkLds {
   }
 };
 
+
 __device__ __forceinline__ i16x4_t lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)p);
 }
 
-template <typename T, int D, int G, int BS, int W, int BPW>
-__global__ __launch_bounds__(64 * W, 8 / (W * BPW)) void attn_chunk_mfma_kernel(
+// PFX = false: prefill chunks (causal, normalised output rows).  PFX = true:
+// the shared-prefix pass -- workgroup (item, kv head) takes up to QT group
+// members against one 128-key split of the group's prefix (no causal mask;
+// every prefix key precedes every member's query) and writes prefix
+// partials.
+template <typename T, int D, int G, int BS, int W, int BPW, bool PFX>
+__global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mfma_kernel(
     const T* __restrict__ q, int64_t q_stride,
     const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
     const int32_t* __restrict__ block_tables, int max_blocks,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ ctx, int seq_begin,
-    int nq_tiles, int num_groups, float scale_log2, T* __restrict__ out, int64_t out_stride) {
+    int nq_tiles, int num_groups, float scale_log2, T* __restrict__ out, int64_t out_stride,
+    PrefixArgs pfx) {
   using M = Mfma32<T>;
   using v8 = typename M::v8;
   using L = ChunkLds<D, W * BPW>;
@@ -598,20 +692,43 @@ __global__ __launch_bounds__(64 * W, 8 / (W * BPW)) void attn_chunk_mfma_kernel(
   // all query tiles of one group run on one XCD and share its L2 copy of
   // the group's K/V, and consecutive groups alternate XCDs.
   const int wg = (int)blockIdx.x;
-  const int slot = wg / kXcds;
-  const int grp = (slot / nq_tiles) * kXcds + wg % kXcds;
-  if (grp >= num_groups) return;
-  const int kvh = grp % num_kv_heads;
-  const int seq = seq_begin + grp / num_kv_heads;
-  const int q0 = cu[seq];
-  const int qlen = cu[seq + 1] - q0;
-  const int qt0 = (slot % nq_tiles) * QT;
-  if (qt0 >= qlen) return;
-  const int ctxlen = min(ctx[seq], max_blocks * BS);
-  const int pos0 = ctxlen - qlen;                                    // position of chunk row 0
-  const int kend = max(0, min(ctxlen, pos0 + min(qt0 + QT, qlen)));  // keys [0, kend)
-  if (kend <= 0) return;
-  const int ntiles = (kend + KT - 1) / KT;
+  int kvh, seq, q0, qlen, qt0, pos0, kb0, kend, mbeg = 0, split = 0;
+  if constexpr (PFX) {
+    const int item = wg / num_kv_heads;
+    kvh = wg % num_kv_heads;
+    if (item >= pfx.max_items) return;
+    const int4 it = *reinterpret_cast<const int4*>(pfx.items + 4 * item);
+    // unused item (leader < 0); rows beyond num_groups (= decode rows) and
+    // splits beyond the partial buffers are ignored
+    if (it.x < 0 || it.x >= num_groups || it.w < 0 || it.w >= kPrefixMaxSplits) return;
+    seq = it.x;                                 // the group leader's block table
+    mbeg = it.y;
+    qlen = it.z;                                // members in this item (<= QT)
+    split = it.w;
+    q0 = 0;
+    qt0 = 0;
+    const int pkeys = min(min(pfx.blocks[seq], max_blocks), kPrefixMaxBlocks) * BS;
+    kb0 = split * kPrefixKeysPerSplit;
+    kend = min(pkeys, kb0 + kPrefixKeysPerSplit);
+    pos0 = 0x3fffffff;                          // queries follow every prefix key
+    if (kb0 >= kend || qlen <= 0) return;
+  } else {
+    const int slot = wg / kXcds;
+    const int grp = (slot / nq_tiles) * kXcds + wg % kXcds;
+    if (grp >= num_groups) return;
+    kvh = grp % num_kv_heads;
+    seq = seq_begin + grp / num_kv_heads;
+    q0 = cu[seq];
+    qlen = cu[seq + 1] - q0;
+    qt0 = (slot % nq_tiles) * QT;
+    if (qt0 >= qlen) return;
+    const int ctxlen = min(ctx[seq], max_blocks * BS);
+    pos0 = ctxlen - qlen;                                      // position of chunk row 0
+    kb0 = 0;
+    kend = max(0, min(ctxlen, pos0 + min(qt0 + QT, qlen)));    // keys [0, kend)
+    if (kend <= 0) return;
+  }
+  const int ntiles = (kend - kb0 + KT - 1) / KT;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31;        // this lane's query column / key row
@@ -623,11 +740,16 @@ __global__ __launch_bounds__(64 * W, 8 / (W * BPW)) void attn_chunk_mfma_kernel(
   const int row = 32 * wave + lr;
   const int qtok = qt0 + row % QT;
   const int qg = row / QT;
-  const int qpos = pos0 + qtok;
+  const int qpos = PFX ? pos0 : pos0 + qtok;
+  int qrow = PFX ? pfx.members[mbeg + min(qtok, qlen - 1)] : q0 + min(qtok, qlen - 1);
+  bool qrow_ok = true;
+  if constexpr (PFX) {
+    qrow_ok = qrow >= 0 && qrow < num_groups;
+    qrow = qrow_ok ? qrow : seq;
+  }
   v8 qf[QSTEPS];
   {
-    const T* qp = q + (int64_t)(q0 + min(qtok, qlen - 1)) * q_stride +
-                  (int64_t)(kvh * G + qg) * D + 8 * h;
+    const T* qp = q + (int64_t)qrow * q_stride + (int64_t)(kvh * G + qg) * D + 8 * h;
 #pragma unroll
     for (int st = 0; st < QSTEPS; ++st) qf[st] = __builtin_bit_cast(v8, load16(qp + 16 * st));
   }
@@ -813,7 +935,7 @@ __global__ __launch_bounds__(64 * W, 8 / (W * BPW)) void attn_chunk_mfma_kernel(
   // One step: start loading the next tile into the other stage, compute
   // this one, then wait for the loads and make them visible to all.
   auto step = [&](auto MaskT, uint16_t* Kc, uint16_t* Vc, uint16_t* Kn, uint16_t* Vn, int it) {
-    const int k0 = it * KT;
+    const int k0 = kb0 + it * KT;
     const bool more = it + 1 < ntiles;
     if (more) stage(Kn, Vn, k0 + KT);
     compute(MaskT, Kc, Vc, k0);
@@ -824,16 +946,17 @@ __global__ __launch_bounds__(64 * W, 8 / (W * BPW)) void attn_chunk_mfma_kernel(
       __syncthreads();
     }
   };
-  stage(Ks0, Vs0, 0);
+  stage(Ks0, Vs0, kb0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (KT > kend) {
-    zero_tail(Vs0, 0);
+  if (kb0 + KT > kend) {
+    zero_tail(Vs0, kb0);
     __syncthreads();
   }
   // Tiles [0, nfull) need no mask for any row of the workgroup (its
   // earliest row sits at position pos0 + qt0); the rest may.
-  const int nfull = min(ntiles, min(kend, pos0 + qt0 + 1) / KT);
+  const int nfull = PFX ? (kend - kb0) / KT
+                        : min(ntiles, min(kend, pos0 + qt0 + 1) / KT);
   const std::false_type plain{};
   const std::true_type masked{};
   int it = 0;
@@ -855,8 +978,25 @@ __global__ __launch_bounds__(64 * W, 8 / (W * BPW)) void attn_chunk_mfma_kernel(
   // Row sum over both halves of the wavefront, then write this lane's
   // query row: O^T slot i of block b is dim 32 b + 8 (i / 4) + 4 h + i % 4.
   l_run += __shfl_xor(l_run, 32);
-  if (qtok >= qlen) return;
+  if (qtok >= qlen || !qrow_ok) return;
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  if constexpr (PFX) {
+    const int H = num_kv_heads * G;
+    const int64_t base = ((int64_t)qrow * H + kvh * G + qg) * kPrefixMaxSplits + split;
+    if (h == 0) {
+      pfx.ml[base * 2] = m_run;
+      pfx.ml[base * 2 + 1] = l_run;
+    }
+    float* ap = pfx.acc + base * D + 4 * h;
+#pragma unroll
+    for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        *reinterpret_cast<float4*>(ap + 32 * b + 8 * g4) =
+            make_float4(o[b][4 * g4] * inv, o[b][4 * g4 + 1] * inv, o[b][4 * g4 + 2] * inv,
+                        o[b][4 * g4 + 3] * inv);
+    return;
+  }
   T* op = out + (int64_t)(q0 + qtok) * out_stride + (int64_t)(kvh * G + qg) * D + 4 * h;
 #pragma unroll
   for (int b = 0; b < DBLK; ++b)
@@ -952,7 +1092,8 @@ static AttnPlan plan_decode(int num_decodes, int num_heads, int num_kv_heads, in
     // NBUF - 1 blocks (8 KiB each at the Qwen3 shape) in flight.
     p.nbuf = env_int("LV_ATTN_NBUF", 2) == 4 ? 4 : 2;
     p.num_wgs = env_int("LV_ATTN_PERSIST_WGS", device_cu_count() * (num_kv_heads == 1 ? 4 : 1));
-    p.off_bytes = align256(sizeof(int32_t) * (size_t)(num_decodes + 1));
+    // block offsets [num_decodes + 1] and shared-prefix skips [num_decodes]
+    p.off_bytes = align256(sizeof(int32_t) * (size_t)(2 * num_decodes + 1));
     p.ml_bytes = align256(sizeof(float) * 2 * (size_t)p.num_wgs * 2 * num_heads);
     p.acc_bytes = align256(sizeof(float) * (size_t)p.num_wgs * 2 * num_heads * head_dim);
     return p;
@@ -996,19 +1137,30 @@ static void launch_persistent(const void* q, int64_t q_stride, const void* kc, c
                               int num_kv_heads, int64_t num_cache_blocks, const int32_t* bt,
                               int max_blocks, const int32_t* ctx, int num_seqs, float scale_log2,
                               void* out, int64_t out_stride, const AttnPlan& p, char* ws,
-                              hipStream_t st) {
+                              const PrefixArgs& pfx, hipStream_t st) {
   int32_t* ws_off = (int32_t*)ws;
   float* ws_ml = (float*)(ws + p.off_bytes);
   float* ws_acc = (float*)(ws + p.off_bytes + p.ml_bytes);
-  const size_t lds = sizeof(int32_t) * (size_t)(num_seqs + 1);
+  // (the entry point admits a prefix only for bf16 / fp16, head_dim 64 / 128)
+  if constexpr (!std::is_same<T, float>::value && (D == 64 || D == 128) && BS == 16) {
+    if (pfx.blocks && pfx.max_items > 0) {
+      // shared prefixes first: their partials are read by the two kernels below
+      hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16, 4, 1, true>),
+                         dim3((unsigned)(pfx.max_items * num_kv_heads)), dim3(256), 0, st,
+                         (const T*)q, q_stride, (const T*)kc, (const T*)vc, num_kv_heads,
+                         num_cache_blocks, bt, max_blocks, nullptr, ctx, 0, 1, num_seqs, scale_log2,
+                         (T*)out, out_stride, pfx);
+    }
+  }
+  const size_t lds = sizeof(int32_t) * (size_t)(num_seqs + 1 + (pfx.blocks ? num_seqs : 0));
   hipLaunchKernelGGL((attn_decode_persistent_kernel<T, D, G, BS, NT, NBUF>), dim3(p.num_wgs),
                      dim3(64 * num_kv_heads), lds, st, (const T*)q, q_stride, (const T*)kc,
                      (const T*)vc, num_kv_heads, num_cache_blocks, bt, max_blocks, ctx, num_seqs,
-                     scale_log2, (T*)out, out_stride, ws_off, ws_acc, ws_ml);
+                     scale_log2, (T*)out, out_stride, ws_off, ws_acc, ws_ml, pfx);
   hipLaunchKernelGGL((attn_persist_reduce_kernel<T, D>), dim3(num_seqs, num_kv_heads * G),
                      dim3(D), 0, st, (const int32_t*)ws_off, num_seqs, p.num_wgs,
                      num_kv_heads * G, (const float*)ws_acc, (const float*)ws_ml, (T*)out,
-                     out_stride);
+                     out_stride, pfx, BS);
 }
 
 // Everything one launch needs besides the dtype / shape template arguments.
@@ -1017,6 +1169,7 @@ struct LaunchArgs {
   int64_t num_cache_blocks; const int32_t* bt; int max_blocks; const int32_t* cu; int num_seqs;
   const int32_t* ctx; int row_begin; int n_rows; float scale_log2; void* out; int64_t out_stride;
   hipStream_t st;
+  PrefixArgs pfx;   // decode rows' shared-prefix pass (blocks == nullptr: none)
 };
 
 template <typename T, int D, int G, int BS>
@@ -1028,7 +1181,7 @@ static void launch(const LaunchArgs& a, const AttnPlan& p, char* ws) {
   launch_persistent<T, D, G, BS, NT_, NB_>(a.q, a.q_stride, a.kc, a.vc, a.num_kv_heads,        \
                                            a.num_cache_blocks, a.bt, a.max_blocks, a.ctx,       \
                                            a.n_rows, a.scale_log2, a.out, a.out_stride, p, ws,  \
-                                           a.st)
+                                           a.pfx, a.st)
     if (p.nt && p.nbuf == 4) LV_PERSIST(true, 4);
     else if (p.nt) LV_PERSIST(true, 2);
     else if (p.nbuf == 4) LV_PERSIST(false, 4);
@@ -1087,10 +1240,11 @@ static void launch_chunk_kernel_w(const LaunchArgs& a, const int32_t* cu, int se
   const int nq = (max_query_len + QT - 1) / QT;
   const int groups = a.num_kv_heads * n_seqs;
   const int64_t wgs = (int64_t)((groups + kXcds - 1) / kXcds) * kXcds * nq;
-  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16, W, BPW>), dim3((unsigned)wgs),
+  hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16, W, BPW, false>), dim3((unsigned)wgs),
                      dim3(64 * W), 0, a.st, (const T*)a.q, a.q_stride, (const T*)a.kc,
                      (const T*)a.vc, a.num_kv_heads, a.num_cache_blocks, a.bt, a.max_blocks, cu,
-                     a.ctx, seq_begin, nq, groups, a.scale_log2, (T*)a.out, a.out_stride);
+                     a.ctx, seq_begin, nq, groups, a.scale_log2, (T*)a.out, a.out_stride,
+                     PrefixArgs{});
 }
 
 // Chunk workgroup shape (LV_ATTN_CHUNK_CFG): 1 = 4 wavefronts x 64-key tiles
@@ -1155,18 +1309,17 @@ extern "C" size_t lv_paged_attention_workspace_size(int32_t num_seqs, int32_t nu
   return a.bytes() > b.bytes() ? a.bytes() : b.bytes();
 }
 
-extern "C" int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
-                                  const void* key_cache_dev, const void* value_cache_dev,
-                                  int64_t num_cache_blocks,
-                                  const int32_t* block_tables_dev, int32_t max_blocks,
-                                  const int32_t* cu_seqlens_dev, const int32_t* context_lens_dev,
-                                  int32_t num_seqs, int32_t num_decodes, int64_t num_tokens,
-                                  int32_t max_query_len, int32_t num_heads, int32_t num_kv_heads,
-                                  int32_t head_dim, int32_t block_size, float scale, void* out_dev,
-                                  int64_t out_stride_t, void* workspace_dev,
-                                  size_t workspace_bytes, lv_dtype dtype, void* stream) {
+static int paged_attention_impl(const void* query_dev, int64_t q_stride_t,
+                                const void* key_cache_dev, const void* value_cache_dev,
+                                int64_t num_cache_blocks, const int32_t* block_tables_dev,
+                                int32_t max_blocks, const int32_t* cu_seqlens_dev,
+                                const int32_t* context_lens_dev, int32_t num_seqs,
+                                int32_t num_decodes, int64_t num_tokens, int32_t max_query_len,
+                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t block_size, float scale, void* out_dev,
+                                int64_t out_stride_t, void* workspace_dev, size_t workspace_bytes,
+                                lv_dtype dtype, void* stream, const lv::PrefixArgs* pfx) {
   using namespace lv;
-  clear_error();
   LV_REQUIRE(dtype == LV_F32 || dtype == LV_F16 || dtype == LV_BF16,
              "lv_paged_attention: bad dtype");
   LV_REQUIRE(num_seqs >= 0 && num_decodes >= 0 && num_decodes <= num_seqs,
@@ -1213,7 +1366,17 @@ extern "C" int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
     a.num_seqs = num_decodes;
     a.row_begin = 0;
     a.n_rows = num_decodes;
+    if (pfx) {
+      if (!p.persistent || dtype == LV_F32 || (head_dim != 64 && head_dim != 128) ||
+          block_size != 16 || !(G == 1 || G == 2 || G == 4 || G == 8) ||
+          num_decodes > kPrefixMaxRows) {
+        set_error("lv_paged_attention_prefix: no shared-prefix path for this shape");
+        return LV_ERR_UNSUPPORTED;
+      }
+      a.pfx = *pfx;
+    }
     const int rc = dispatch(dtype, head_dim, G, block_size, a, p, (char*)workspace_dev);
+    a.pfx = PrefixArgs{};
     if (rc != LV_OK) return rc;
   }
   if (num_decodes < num_seqs && dtype != LV_F32 && (head_dim == 64 || head_dim == 128) &&
@@ -1240,4 +1403,72 @@ extern "C" int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
     if (rc != LV_OK) return rc;
   }
   return check_launch("lv_paged_attention");
+}
+
+extern "C" int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
+                                  const void* key_cache_dev, const void* value_cache_dev,
+                                  int64_t num_cache_blocks,
+                                  const int32_t* block_tables_dev, int32_t max_blocks,
+                                  const int32_t* cu_seqlens_dev, const int32_t* context_lens_dev,
+                                  int32_t num_seqs, int32_t num_decodes, int64_t num_tokens,
+                                  int32_t max_query_len, int32_t num_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t block_size, float scale, void* out_dev,
+                                  int64_t out_stride_t, void* workspace_dev,
+                                  size_t workspace_bytes, lv_dtype dtype, void* stream) {
+  lv::clear_error();
+  return paged_attention_impl(query_dev, q_stride_t, key_cache_dev, value_cache_dev,
+                              num_cache_blocks, block_tables_dev, max_blocks, cu_seqlens_dev,
+                              context_lens_dev, num_seqs, num_decodes, num_tokens, max_query_len,
+                              num_heads, num_kv_heads, head_dim, block_size, scale, out_dev,
+                              out_stride_t, workspace_dev, workspace_bytes, dtype, stream,
+                              nullptr);
+}
+
+extern "C" size_t lv_paged_attention_prefix_workspace_size(int32_t num_decodes,
+                                                           int32_t num_heads,
+                                                           int32_t head_dim) {
+  if (num_decodes <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  const size_t n = (size_t)num_decodes * num_heads * lv::kPrefixMaxSplits;
+  return lv::align256(n * 2 * sizeof(float)) + lv::align256(n * head_dim * sizeof(float));
+}
+
+extern "C" int lv_paged_attention_prefix(
+    const void* query_dev, int64_t q_stride_t, const void* key_cache_dev,
+    const void* value_cache_dev, int64_t num_cache_blocks, const int32_t* block_tables_dev,
+    int32_t max_blocks, const int32_t* cu_seqlens_dev, const int32_t* context_lens_dev,
+    int32_t num_seqs, int32_t num_decodes, int64_t num_tokens, int32_t max_query_len,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+    void* out_dev, int64_t out_stride_t, void* workspace_dev, size_t workspace_bytes,
+    const int32_t* prefix_blocks_dev, const int32_t* prefix_items_dev, int32_t max_items,
+    const int32_t* prefix_members_dev, void* prefix_workspace_dev, size_t prefix_workspace_bytes,
+    lv_dtype dtype, void* stream) {
+  using namespace lv;
+  clear_error();
+  LV_REQUIRE(num_decodes >= 1 && num_decodes <= kPrefixMaxRows,
+             "lv_paged_attention_prefix: num_decodes must be in [1, %d]", kPrefixMaxRows);
+  LV_REQUIRE(prefix_blocks_dev && prefix_members_dev && max_items >= 0 &&
+                 (prefix_items_dev || max_items == 0),
+             "lv_paged_attention_prefix: null prefix description");
+  LV_REQUIRE((reinterpret_cast<uintptr_t>(prefix_items_dev) & 15) == 0,
+             "lv_paged_attention_prefix: prefix_items must be 16-byte aligned");
+  const size_t need = lv_paged_attention_prefix_workspace_size(num_decodes, num_heads, head_dim);
+  if (!prefix_workspace_dev || prefix_workspace_bytes < need ||
+      (reinterpret_cast<uintptr_t>(prefix_workspace_dev) & 255) != 0) {
+    set_error("lv_paged_attention_prefix: prefix workspace needs %zu bytes (256-B aligned), "
+              "got %zu", need, prefix_workspace_bytes);
+    return LV_ERR_WORKSPACE;
+  }
+  const size_t n = (size_t)num_decodes * num_heads * kPrefixMaxSplits;
+  PrefixArgs pa;
+  pa.blocks = prefix_blocks_dev;
+  pa.items = prefix_items_dev;
+  pa.members = prefix_members_dev;
+  pa.max_items = max_items;
+  pa.ml = (float*)prefix_workspace_dev;
+  pa.acc = (float*)((char*)prefix_workspace_dev + align256(n * 2 * sizeof(float)));
+  return paged_attention_impl(query_dev, q_stride_t, key_cache_dev, value_cache_dev,
+                              num_cache_blocks, block_tables_dev, max_blocks, cu_seqlens_dev,
+                              context_lens_dev, num_seqs, num_decodes, num_tokens, max_query_len,
+                              num_heads, num_kv_heads, head_dim, block_size, scale, out_dev,
+                              out_stride_t, workspace_dev, workspace_bytes, dtype, stream, &pa);
 }

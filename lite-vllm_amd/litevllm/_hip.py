@@ -18,7 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 LV_F32, LV_F16, LV_BF16 = 0, 1, 2
 LV_ACT_NONE, LV_ACT_SILU_MUL = 0, 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Every symbol the header declares, with (restype, argtypes).
 _c_i32, _c_i64, _c_f32, _c_p, _c_sz = (
@@ -58,6 +58,22 @@ SIGNATURES: dict[str, tuple] = {
         _c_i32, _c_f32,               # block_size, scale
         _c_p, _c_i64,                 # out, out_stride_t
         _c_p, _c_sz,                  # workspace, workspace_bytes
+        ctypes.c_int, _c_p,           # dtype, stream
+    ]),
+    "lv_paged_attention_prefix_workspace_size": (_c_sz, [_c_i32, _c_i32, _c_i32]),
+    "lv_paged_attention_prefix": (ctypes.c_int, [
+        _c_p, _c_i64,                 # query, q_stride_t
+        _c_p, _c_p, _c_i64,           # key_cache, value_cache, num_cache_blocks
+        _c_p, _c_i32,                 # block_tables, max_blocks
+        _c_p, _c_p,                   # cu_seqlens, context_lens
+        _c_i32, _c_i32, _c_i64,       # num_seqs, num_decodes, num_tokens
+        _c_i32,                       # max_query_len
+        _c_i32, _c_i32, _c_i32,       # num_heads, num_kv_heads, head_dim
+        _c_i32, _c_f32,               # block_size, scale
+        _c_p, _c_i64,                 # out, out_stride_t
+        _c_p, _c_sz,                  # workspace, workspace_bytes
+        _c_p, _c_p, _c_i32,           # prefix_blocks, prefix_items, max_items
+        _c_p, _c_p, _c_sz,            # prefix_members, prefix_workspace, its bytes
         ctypes.c_int, _c_p,           # dtype, stream
     ]),
     "lv_sample_workspace_size": (ctypes.c_size_t, [_c_i64, _c_i64]),

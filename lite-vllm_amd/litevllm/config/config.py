@@ -93,6 +93,9 @@ class CacheConfig:
     num_cpu_blocks: int = 0
     gpu_memory_utilization: float = 0.85
     enable_prefix_caching: bool = False
+    # decode rows whose block tables start with the same blocks read that
+    # shared prefix once per group in attention
+    shared_prefix_attention: bool = True
 
 
 @dataclass

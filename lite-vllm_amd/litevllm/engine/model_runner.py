@@ -71,7 +71,8 @@ class InputMetadata:
                  sample_seqs: Optional[list[Sequence]] = None,
                  sample_groups: Optional[list[SequenceGroup]] = None,
                  num_decodes: int = 0, num_context_tokens: int = 0,
-                 num_context_blocks: int = 0, graph_batch: Optional[int] = None) -> None:
+                 num_context_blocks: int = 0, graph_batch: Optional[int] = None,
+                 prefix_stats: tuple[int, int] = (0, 0)) -> None:
         self.input_ids = input_ids
         self.positions = positions
         self.slot_mapping = slot_mapping
@@ -87,6 +88,9 @@ class InputMetadata:
         self.num_context_tokens = num_context_tokens   # sum of context lengths (host)
         self.num_context_blocks = num_context_blocks   # sum of block-table lengths (host)
         self.graph_batch = graph_batch                 # padded batch of a graph replay
+        # shared-prefix pass of this step: block reads it saves, and the
+        # (member row, 128-key split) partials it writes and merges
+        self.prefix_saved_blocks, self.prefix_partial_rows = prefix_stats
 
 
 @dataclass
@@ -166,6 +170,83 @@ def build_step(seq_groups: list[SequenceGroup], block_manager) -> StepDescriptor
                            uses_device_tokens)
 
 
+# Shared-prefix attention: work items per step (graph-static) and the block
+# reads a step must save before the extra pass pays for itself (the pass
+# costs about what reading a thousand 16-token blocks of all kv heads does).
+PREFIX_MAX_ITEMS = 64
+PREFIX_MIN_SAVED_BLOCKS = int(os.environ.get("LV_PREFIX_MIN_BLOCKS", "1024"))
+
+
+def find_shared_prefixes(descs: np.ndarray, block_ids: np.ndarray, num_decodes: int,
+                         block_size: int, group_size: int, max_items: int = PREFIX_MAX_ITEMS,
+                         min_saved: Optional[int] = None) -> list[tuple[np.ndarray, int]]:
+    """Groups of decode rows whose block tables start with the same physical
+    blocks (prefix-cache hits on a common prompt, forked sequences) and the
+    length of each group's common run of blocks: at most
+    ops.PREFIX_MAX_BLOCKS and never past any member's context
+    (prefix * block_size <= context length).  Returns [] unless reading each
+    prefix once saves at least ``min_saved`` block reads (default
+    PREFIX_MIN_SAVED_BLOCKS); keeps the groups with the largest savings
+    within ``max_items`` work items."""
+    if min_saved is None:
+        min_saved = PREFIX_MIN_SAVED_BLOCKS
+    if num_decodes < 2 or block_ids.size == 0:
+        return []
+    d = descs[:num_decodes].astype(np.int64)
+    nblk, off = d[:, 2], d[:, 3]
+    cap_row = np.minimum(np.minimum((d[:, 0] + d[:, 1]) // block_size, nblk),
+                         ops.PREFIX_MAX_BLOCKS)
+    rows = np.nonzero(cap_row > 0)[0]
+    if rows.size < 2:
+        return []
+    first = block_ids[off[rows]]
+    order = np.argsort(first, kind="stable")
+    rows, first = rows[order], first[order]
+    head = np.ones(rows.size, dtype=bool)
+    head[1:] = first[1:] != first[:-1]
+    gid = np.cumsum(head) - 1
+    sizes = np.bincount(gid)
+    keep = sizes[gid] >= 2
+    if not keep.any():
+        return []
+    rows, first = rows[keep], first[keep]
+    head = np.ones(rows.size, dtype=bool)
+    head[1:] = first[1:] != first[:-1]
+    starts = np.nonzero(head)[0]
+    gid = np.cumsum(head) - 1
+    sizes = np.diff(np.append(starts, rows.size))
+    leader = rows[starts][gid]
+    cap_g = np.minimum.reduceat(cap_row[rows], starts)
+    j = np.arange(int(cap_g.max()))
+    last = block_ids.size - 1
+    mine = block_ids[np.minimum(off[rows][:, None] + j, last)]
+    lead = block_ids[np.minimum(off[leader][:, None] + j, last)]
+    eq = (mine == lead) | (j >= cap_g[gid][:, None])
+    lcp = np.where(eq.all(1), j.size, np.argmin(eq, axis=1))
+    lcp_g = np.minimum(np.minimum.reduceat(lcp, starts), cap_g)
+    saved = (sizes - 1) * lcp_g
+    if int(saved.sum()) < min_saved:
+        return []
+    groups, items = [], 0
+    for g in np.argsort(-saved, kind="stable"):
+        if lcp_g[g] <= 0:
+            break
+        grp = (rows[starts[g]:starts[g] + sizes[g]], int(lcp_g[g]))
+        need = ops.prefix_items_needed([grp], group_size, block_size)
+        if items + need <= max_items:
+            groups.append(grp)
+            items += need
+    return groups
+
+
+def prefix_stats(groups, block_size: int) -> tuple[int, int]:
+    """(block reads saved, member-split partials) of a list of groups."""
+    saved = sum((len(rows) - 1) * pb for rows, pb in groups)
+    parts = sum(len(rows) * -(-pb * block_size // ops.PREFIX_KEYS_PER_SPLIT)
+                for rows, pb in groups)
+    return saved, parts
+
+
 class _Staging:
     """Grow-only pinned host buffers for one step's packing inputs.  The
     copies out of them are asynchronous, so get() first waits for the
@@ -240,6 +321,27 @@ class DecodeGraphs:
                                                     cc.block_size, self.max_blocks, 1,
                                                     mc.torch_dtype) for b in self.batches)
         self.workspace = torch.empty(max(ws, 256), dtype=torch.uint8, device=dev)
+        # Shared-prefix plan, one static int32 buffer: blocks [n] (padded to
+        # a multiple of 4 so the items stay 16-byte aligned), items
+        # [PREFIX_MAX_ITEMS, 4], members [n].  Every graph reads all of it;
+        # rows and items beyond a graph's batch are skipped by the kernel.
+        self.group_size = mc.num_attention_heads // mc.num_key_value_heads
+        self.use_prefix = cc.shared_prefix_attention and ops.prefix_attention_supported(
+            mc.num_attention_heads, mc.num_key_value_heads, mc.head_dim, cc.block_size,
+            mc.torch_dtype)
+        self._pfx_active = False
+        if self.use_prefix:
+            npad = (n + 3) // 4 * 4
+            self.pfx_buf = torch.zeros(npad + 4 * PREFIX_MAX_ITEMS + n, dtype=torch.int32,
+                                       device=dev)
+            self.pfx_buf[npad:npad + 4 * PREFIX_MAX_ITEMS].view(-1, 4)[:, 0] = -1
+            self.pfx_plan = ops.PrefixPlan(
+                self.pfx_buf[:n], self.pfx_buf[npad:npad + 4 * PREFIX_MAX_ITEMS].view(-1, 4),
+                self.pfx_buf[npad + 4 * PREFIX_MAX_ITEMS:])
+            self.pfx_npad = npad
+            self.pfx_workspace = torch.empty(
+                max(ops.prefix_workspace_size(n, mc.num_attention_heads, mc.head_dim), 256),
+                dtype=torch.uint8, device=dev)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.logits: dict[int, torch.Tensor] = {}
         tmpl = torch.zeros((n, 6), dtype=torch.int32)
@@ -260,6 +362,10 @@ class DecodeGraphs:
         meta = AttentionMetadata(block_tables=v["block_tables"], context_lens=v["context_lens"],
                                  cu_seqlens=v["cu_seqlens"], num_decodes=b, max_query_len=1,
                                  workspace=self.workspace)
+        if self.use_prefix:
+            p = self.pfx_plan
+            meta.prefix = ops.PrefixPlan(p.blocks[:b], p.items, p.members)
+            meta.prefix_workspace = self.pfx_workspace
         r = self.runner
         kv = [r.kv_cache.get_kv(i) for i in range(r.model_config.num_hidden_layers)]
         return r.model(input_ids=v["input_ids"], positions=v["positions"], kv_caches=kv,
@@ -301,13 +407,29 @@ class DecodeGraphs:
         b = next(x for x in self.batches if x >= B)
         nb = st.block_ids.shape[0]
         n_host = len(st.tokens)
-        st32, st64 = staging.get(B * 6 + nb, max(n_host, 1))
+        groups = find_shared_prefixes(st.descs, st.block_ids, B, self.block_size,
+                                      self.group_size) if self.use_prefix else []
+        n_pfx = self.pfx_buf.numel() if (groups or self._pfx_active) else 0
+        st32, st64 = staging.get(B * 6 + nb + n_pfx, max(n_host, 1))
         a32 = st32.numpy()
         a32[:B * 6] = st.descs.reshape(-1)
-        a32[B * 6:] = st.block_ids
+        a32[B * 6:B * 6 + nb] = st.block_ids
         st64.numpy()[:n_host] = st.tokens
         self.descs[:B].view(-1).copy_(st32[:B * 6], non_blocking=True)
-        self.block_ids[:nb].copy_(st32[B * 6:], non_blocking=True)
+        self.block_ids[:nb].copy_(st32[B * 6:B * 6 + nb], non_blocking=True)
+        if n_pfx:
+            # a new plan, or the empty one replacing the previous step's
+            n = self.batches[-1]
+            blocks, items, members = ops.prefix_plan_arrays(
+                groups, n, self.group_size, self.block_size, max_items=PREFIX_MAX_ITEMS,
+                max_members=n)
+            r = a32[B * 6 + nb:]
+            r[:n] = blocks
+            r[n:self.pfx_npad] = 0
+            r[self.pfx_npad:self.pfx_npad + items.size] = items.reshape(-1)
+            r[self.pfx_npad + items.size:] = members
+            self.pfx_buf.copy_(st32[B * 6 + nb:], non_blocking=True)
+            self._pfx_active = bool(groups)
         if n_host:
             self.token_ids[:n_host].copy_(st64[:n_host], non_blocking=True)
         staging.record()
@@ -318,7 +440,8 @@ class DecodeGraphs:
                              sample_seqs=st.sample_seqs, sample_groups=st.sample_groups,
                              num_decodes=B,
                              num_context_tokens=int(st.descs[:, 0].sum() + st.descs[:, 1].sum()),
-                             num_context_blocks=int(nb), graph_batch=b)
+                             num_context_blocks=int(nb), graph_batch=b,
+                             prefix_stats=prefix_stats(groups, self.block_size))
 
     def _pad_rows(self, start: int, b: int) -> None:
         """Descriptors start..b-1 become padding: one token (id 0) at
@@ -400,10 +523,21 @@ class ModelRunner:
         h = max(n_host, 1)                   # keep the id array non-empty
         dev = torch.device(self.device)
         n32 = B * 6 + n_blocks
-        st32, st64 = self._staging.get(n32, h + len(st.logits_rows))
+        plan_arrays = self._prefix_arrays(st)
+        p0 = (n32 + 3) // 4 * 4              # plan after the tables, 16-byte aligned
+        n_all = p0 + sum(a.size for a in plan_arrays[:3]) + 4 if plan_arrays else n32
+        st32, st64 = self._staging.get(n_all, h + len(st.logits_rows))
         a32 = st32.numpy()
         a32[:B * 6] = st.descs.reshape(-1)
         a32[B * 6:n32] = st.block_ids
+        stats = (0, 0)
+        if plan_arrays:
+            blocks, items, members, stats = plan_arrays
+            nd = blocks.size
+            i0 = p0 + (nd + 3) // 4 * 4
+            a32[p0:p0 + nd] = blocks
+            a32[i0:i0 + items.size] = items.reshape(-1)
+            a32[i0 + items.size:i0 + items.size + members.size] = members
         a64 = st64.numpy()
         a64[:n_host] = st.tokens
         a64[h:] = st.logits_rows
@@ -417,13 +551,31 @@ class ModelRunner:
                                  context_lens=packed["context_lens"],
                                  cu_seqlens=packed["cu_seqlens"], num_decodes=st.num_decodes,
                                  max_query_len=st.max_query_len)
+        if plan_arrays:
+            attn.prefix = ops.PrefixPlan(d32[p0:p0 + nd], d32[i0:i0 + items.size].view(-1, 4),
+                                         d32[i0 + items.size:i0 + items.size + members.size])
         return InputMetadata(packed["input_ids"], packed["positions"], packed["slot_mapping"],
                              packed["block_tables"], packed["context_lens"], st.is_prefill,
                              st.seq_ids, attn_metadata=attn, logits_indices=d64[h:],
                              sample_seqs=st.sample_seqs, sample_groups=st.sample_groups,
                              num_decodes=st.num_decodes,
                              num_context_tokens=int(st.descs[:, 0].sum() + st.descs[:, 1].sum()),
-                             num_context_blocks=int(n_blocks))
+                             num_context_blocks=int(n_blocks), prefix_stats=stats)
+
+    def _prefix_arrays(self, st: StepDescriptors):
+        """Host plan of the step's shared decode prefixes, or None."""
+        cc = self.config.cache_config
+        mc = self.model_config
+        if not cc.shared_prefix_attention or st.num_decodes < 2 or not \
+                ops.prefix_attention_supported(mc.num_attention_heads, mc.num_key_value_heads,
+                                               mc.head_dim, cc.block_size, mc.torch_dtype):
+            return None
+        g = mc.num_attention_heads // mc.num_key_value_heads
+        groups = find_shared_prefixes(st.descs, st.block_ids, st.num_decodes, cc.block_size, g)
+        if not groups:
+            return None
+        return (*ops.prefix_plan_arrays(groups, st.num_decodes, g, cc.block_size),
+                prefix_stats(groups, cc.block_size))
 
     @torch.inference_mode()
     def execute_model(self, metadata: InputMetadata) -> torch.Tensor:

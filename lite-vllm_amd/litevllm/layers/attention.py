@@ -32,6 +32,9 @@ class AttentionMetadata:
     num_decodes: int             # leading 1-token sequences
     max_query_len: int
     workspace: Optional[torch.Tensor] = None   # attention scratch owned by a HIP graph
+    # decode rows' shared prefixes, read once per group (lv_paged_attention_prefix)
+    prefix: Optional[ops.PrefixPlan] = None
+    prefix_workspace: Optional[torch.Tensor] = None
 
 
 class PagedAttention:
@@ -61,7 +64,8 @@ class Attention(nn.Module):
             return ops.paged_attention(query, key_cache, value_cache, m.block_tables,
                                        m.context_lens, scale=self.scale, cu_seqlens=m.cu_seqlens,
                                        num_decodes=m.num_decodes, max_query_len=m.max_query_len,
-                                       workspace=m.workspace)
+                                       workspace=m.workspace, prefix=m.prefix,
+                                       prefix_workspace=m.prefix_workspace)
         if is_prefill:
             return self._prefill(query, key, value)
         return ops.paged_attention(query, key_cache, value_cache, block_table, context_lens,

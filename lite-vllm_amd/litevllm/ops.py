@@ -9,7 +9,8 @@ tensors on a ROCm ("cuda") device: there is no CPU path behind these calls.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+import os
+from typing import NamedTuple, Optional
 
 import torch
 
@@ -101,20 +102,119 @@ def kv_scatter(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
 # (3) paged attention
 # ---------------------------------------------------------------------------
 
-_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_workspaces: dict[tuple[int, int, str], torch.Tensor] = {}
 
 
-def _workspace(device: torch.device, nbytes: int) -> Optional[torch.Tensor]:
-    """Per-(device, stream) scratch buffer, grown on demand and reused."""
+def _workspace(device: torch.device, nbytes: int, kind: str = "attn") -> Optional[torch.Tensor]:
+    """Per-(device, stream, kind) scratch buffer, grown on demand and reused."""
     if nbytes == 0:
         return None
     key = (device.index if device.index is not None else torch.cuda.current_device(),
-           _stream(device))
+           _stream(device), kind)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
+
+
+# Shared-prefix pass geometry (lv_paged_attention_prefix): keys per split,
+# most prefix blocks, and query rows (members x GQA heads) per work item.
+PREFIX_KEYS_PER_SPLIT = 128
+PREFIX_MAX_BLOCKS = 128
+PREFIX_ROWS_PER_ITEM = 128
+PREFIX_MAX_DECODES = 7000
+
+
+class PrefixPlan(NamedTuple):
+    """Device description of the decode rows' shared prefixes (the three
+    arrays lv_paged_attention_prefix reads)."""
+    blocks: torch.Tensor    # int32 [num_decodes]: leading blocks of each row in its group's prefix
+    items: torch.Tensor     # int32 [max_items, 4]: leader, first member, members, split
+    members: torch.Tensor   # int32: member rows, one group after another
+
+
+def prefix_plan_arrays(groups, num_decodes: int, group_size: int, block_size: int = 16,
+                       max_items: Optional[int] = None, max_members: Optional[int] = None):
+    """Host (numpy) arrays of a PrefixPlan.
+
+    ``groups``: iterable of (rows, prefix_blocks) -- decode rows whose block
+    tables start with the same ``prefix_blocks`` physical blocks; rows[0] is
+    the leader whose table the prefix pass reads.  ``group_size`` = num_heads
+    // num_kv_heads.  One item per (group, slice of 128 // group_size rows,
+    128-key split); ``max_items`` / ``max_members`` pad the arrays to a fixed
+    size (unused items have leader -1) so they can live in graph-static
+    buffers.  Groups with one row or an empty prefix are dropped.
+    """
+    import numpy as np
+    per_item = PREFIX_ROWS_PER_ITEM // group_size
+    blocks = np.zeros(num_decodes, np.int32)
+    items: list[tuple[int, int, int, int]] = []
+    parts = []
+    base = 0
+    for rows, pblocks in groups:
+        rows = np.asarray(rows, dtype=np.int32).reshape(-1)
+        pblocks = int(pblocks)
+        if pblocks < 0 or pblocks > PREFIX_MAX_BLOCKS:
+            raise ValueError(f"prefix of {pblocks} blocks outside [0, {PREFIX_MAX_BLOCKS}]")
+        n = rows.shape[0]
+        if n < 2 or pblocks == 0:
+            continue
+        parts.append(rows)
+        blocks[rows] = pblocks
+        nsplit = -(-pblocks * block_size // PREFIX_KEYS_PER_SPLIT)
+        leader = int(rows[0])
+        for s0 in range(0, n, per_item):
+            cnt = min(per_item, n - s0)
+            items.extend((leader, base + s0, cnt, sp) for sp in range(nsplit))
+        base += n
+    members = np.concatenate(parts) if parts else np.zeros(0, np.int32)
+    if members.size and (members.min() < 0 or members.max() >= num_decodes
+                         or np.unique(members).size != members.size):
+        raise ValueError("a group row is out of range or in two groups")
+    if max_items is not None:
+        if len(items) > max_items:
+            raise ValueError(f"{len(items)} prefix items exceed max_items={max_items}")
+        items += [(-1, 0, 0, 0)] * (max_items - len(items))
+    if max_members is not None:
+        if members.size > max_members:
+            raise ValueError(f"{members.size} members exceed max_members={max_members}")
+        members = np.concatenate([members, np.zeros(max_members - members.size, np.int32)])
+    items_a = np.asarray(items, np.int32).reshape(-1, 4)
+    members_a = members.astype(np.int32) if members.size else np.zeros(1, np.int32)
+    return blocks, items_a, members_a
+
+
+def prefix_attention_supported(num_heads: int, num_kv_heads: int, head_dim: int,
+                               block_size: int, dtype: torch.dtype) -> bool:
+    """Shapes lv_paged_attention_prefix serves (else LV_ERR_UNSUPPORTED)."""
+    g = num_heads // max(num_kv_heads, 1)
+    return (dtype in (torch.bfloat16, torch.float16) and head_dim in (64, 128)
+            and block_size == 16 and num_heads % max(num_kv_heads, 1) == 0
+            and g in (1, 2, 4, 8) and 1 <= num_kv_heads <= 8
+            and os.environ.get("LV_ATTN_DECODE_KERNEL", "")[:1] != "r")
+
+
+def prefix_workspace_size(num_decodes: int, num_heads: int, head_dim: int) -> int:
+    """Bytes of prefix scratch lv_paged_attention_prefix needs."""
+    return int(_hip.load().lv_paged_attention_prefix_workspace_size(num_decodes, num_heads,
+                                                                    head_dim))
+
+
+def prefix_items_needed(groups, group_size: int, block_size: int = 16) -> int:
+    """Work items prefix_plan_arrays makes for these groups."""
+    per_item = PREFIX_ROWS_PER_ITEM // group_size
+    return sum(-(-len(rows) // per_item) * -(-int(pb) * block_size // PREFIX_KEYS_PER_SPLIT)
+               for rows, pb in groups if len(rows) >= 2 and pb > 0)
+
+
+def prefix_plan(groups, num_decodes: int, group_size: int, device, block_size: int = 16,
+                max_items: Optional[int] = None, max_members: Optional[int] = None) -> PrefixPlan:
+    """PrefixPlan on ``device`` (see prefix_plan_arrays)."""
+    blocks, items, members = prefix_plan_arrays(groups, num_decodes, group_size, block_size,
+                                                max_items, max_members)
+    return PrefixPlan(torch.from_numpy(blocks).to(device), torch.from_numpy(items).to(device),
+                      torch.from_numpy(members).to(device))
 
 
 def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
@@ -123,7 +223,9 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
                     cu_seqlens: Optional[torch.Tensor] = None,
                     num_decodes: Optional[int] = None, max_query_len: int = 1,
                     out: Optional[torch.Tensor] = None,
-                    workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    workspace: Optional[torch.Tensor] = None,
+                    prefix: Optional[PrefixPlan] = None,
+                    prefix_workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Attention of every query row over its sequence's paged K/V.
 
     Reference: litevllm/layers/attention.py:91-139 (decode) and 141-151
@@ -133,7 +235,9 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
     decodes); the first ``num_decodes`` sequences must be 1-token decodes.
     ``workspace`` (uint8, at least paged_attention_workspace_size bytes) is
     used instead of the per-stream scratch buffer when given: a captured HIP
-    graph must own the memory its kernels read.
+    graph must own the memory its kernels read.  ``prefix`` (a PrefixPlan)
+    selects lv_paged_attention_prefix: the decode rows' shared prefixes are
+    read once per group; ``prefix_workspace`` is its scratch as above.
     """
     dev = key_cache.device
     for n, t in (("query", query), ("key_cache", key_cache), ("value_cache", value_cache),
@@ -186,12 +290,40 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
         ws = workspace if ws_bytes > 0 else None
     else:
         ws = _workspace(dev, ws_bytes)
-    rc = lib.lv_paged_attention(
+    if prefix is None:
+        rc = lib.lv_paged_attention(
+            _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache), n_blocks,
+            _ptr(block_tables), max_blocks, _ptr(cu_seqlens), _ptr(context_lens),
+            B, num_decodes, T, max_query_len, H, hkv, D, bs, float(scale),
+            _ptr(out), out.stride(0), _ptr(ws), 0 if ws is None else ws.numel(), dt,
+            _stream(dev))
+        _hip.check(rc, "lv_paged_attention")
+        return out
+    for n, t in zip(("prefix.blocks", "prefix.items", "prefix.members"), prefix):
+        _require_device(n, t, dev)
+    _check_int("prefix.blocks", prefix.blocks, torch.int32, 1)
+    _check_int("prefix.items", prefix.items, torch.int32, 2)
+    _check_int("prefix.members", prefix.members, torch.int32, 1)
+    if prefix.blocks.shape[0] != num_decodes or prefix.items.shape[1] != 4:
+        raise RuntimeError("prefix.blocks must have num_decodes entries and prefix.items 4 columns")
+    pws_bytes = int(lib.lv_paged_attention_prefix_workspace_size(num_decodes, H, D))
+    if prefix_workspace is not None:
+        _require_device("prefix_workspace", prefix_workspace, dev)
+        if prefix_workspace.dtype != torch.uint8 or not prefix_workspace.is_contiguous() or \
+                prefix_workspace.numel() < pws_bytes:
+            raise RuntimeError(
+                f"prefix_workspace must be a contiguous uint8 tensor of >= {pws_bytes} bytes")
+        pws = prefix_workspace
+    else:
+        pws = _workspace(dev, pws_bytes, "prefix")
+    rc = lib.lv_paged_attention_prefix(
         _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache), n_blocks,
         _ptr(block_tables), max_blocks, _ptr(cu_seqlens), _ptr(context_lens),
         B, num_decodes, T, max_query_len, H, hkv, D, bs, float(scale),
-        _ptr(out), out.stride(0), _ptr(ws), 0 if ws is None else ws.numel(), dt, _stream(dev))
-    _hip.check(rc, "lv_paged_attention")
+        _ptr(out), out.stride(0), _ptr(ws), 0 if ws is None else ws.numel(),
+        _ptr(prefix.blocks), _ptr(prefix.items), prefix.items.shape[0], _ptr(prefix.members),
+        _ptr(pws), 0 if pws is None else pws.numel(), dt, _stream(dev))
+    _hip.check(rc, "lv_paged_attention_prefix")
     return out
 
 

@@ -123,26 +123,37 @@ def summarize_counters(pmc_dir: str) -> str:
             cur.append((name, vals))
     if cur:
         steps.append(cur)
+    def is_prefix_pass(n: str) -> bool:
+        return "attn_chunk_mfma_kernel" in n and n.rstrip().endswith("true>")
+
+    def is_chunk(n: str) -> bool:
+        return "attn_chunk_mfma_kernel" in n and not is_prefix_pass(n)
+
+    # One decode-attention call: [shared-prefix pass] + persistent kernel +
+    # reduce kernel, summed.
     pairs: list[dict[str, float]] = []
     for st in steps:
-        if any("attn_chunk_mfma_kernel" in n for n, _ in st):
+        if any(is_chunk(n) for n, _ in st):
             continue
-        acc = None
+        acc, walked = None, False
         for n, vals in st:
-            if "attn_decode_persistent_kernel" in n:
+            if is_prefix_pass(n) or ("attn_decode_persistent_kernel" in n and walked) or \
+                    ("attn_decode_persistent_kernel" in n and acc is None):
                 if acc is not None:
                     pairs.append(acc)
-                acc = dict(vals)
-            elif "attn_persist_reduce_kernel" in n and acc is not None:
+                acc, walked = dict(vals), "attn_decode_persistent_kernel" in n
+            elif acc is not None and ("attn_decode_persistent_kernel" in n
+                                      or "attn_persist_reduce_kernel" in n):
+                walked = walked or "attn_decode_persistent_kernel" in n
                 for c, v in vals.items():
                     acc[c] = acc.get(c, 0.0) + v
         if acc is not None:
             pairs.append(acc)
     out = [f"dispatches with counters: {len(order)}; decode-only steps: "
-           f"{sum(1 for st in steps if not any('attn_chunk_mfma_kernel' in n for n, _ in st))}; "
-           f"decode-attention launch pairs in them: {len(pairs)}", ""]
+           f"{sum(1 for st in steps if not any(is_chunk(n) for n, _ in st))}; "
+           f"decode-attention calls in them: {len(pairs)}", ""]
     if pairs:
-        out.append("| counter | mean per decode-attention launch pair (decode-only steps) |")
+        out.append("| counter | mean per decode-attention call (decode-only steps) |")
         out.append("|---|---|")
         for c in counters:
             vals = [p[c] for p in pairs if c in p]

@@ -165,6 +165,46 @@ def test_qwen3_chunked_prefix_cached_matches_cpu_oracle(device, dtype, min_margi
     assert compared >= min_compared
 
 
+def test_shared_prefix_attention_in_the_engine(device, monkeypatch):
+    """The prefix-cached Qwen3 run above with the shared-prefix attention
+    pass forced on (its threshold lowered to one saved block): decode rows
+    of prompts sharing the cached 96-token prefix read it once per group,
+    in decode-graph replays and in mixed steps alike, and the greedy tokens
+    still equal the CPU oracle's to the same margin."""
+    _say("qwen3 small bf16 shared-prefix attention in the engine")
+    from litevllm.engine import model_runner as mr
+    monkeypatch.setattr(mr, "PREFIX_MIN_SAVED_BLOCKS", 1)
+    used = {"graph": 0, "eager": 0}
+    orig_find = mr.find_shared_prefixes
+    graph_prepare = mr.DecodeGraphs.prepare
+
+    def spy(*a, **k):
+        groups = orig_find(*a, **k)
+        if groups:
+            used["graph" if spy.in_graph else "eager"] += 1
+        return groups
+    spy.in_graph = False
+
+    def prepare(self, *a, **k):
+        spy.in_graph = True
+        try:
+            return graph_prepare(self, *a, **k)
+        finally:
+            spy.in_graph = False
+    monkeypatch.setattr(mr, "find_shared_prefixes", spy)
+    monkeypatch.setattr(mr.DecodeGraphs, "prepare", prepare)
+    prompts = _qwen3_prompts()
+    llm = LLM("tiny-qwen3", dtype="bfloat16", load_format="dummy", hf_overrides=QWEN3_SMALL,
+              skip_tokenizer_init=True, num_gpu_blocks=512, chunk_size=64,
+              max_num_batched_tokens=256, enable_prefix_caching=True)
+    assert llm.engine.model_runner.graphs.use_prefix
+    sp = SamplingParams(temperature=0.0, max_tokens=20, ignore_eos=True)
+    outs = llm.generate(prompt_token_ids=prompts, sampling_params=sp)
+    assert all(o.num_output_tokens == 20 for o in outs)
+    assert used["graph"] > 0 and used["eager"] > 0, used
+    assert _compare_with_oracle(llm, prompts, outs, 20, 0.08, use_qk_norm=True) >= 6
+
+
 def test_sampling_with_temperature_is_seeded(device):
     _say("seeded temperature sampling")
     cfg = dict(TINY_LLAMA, vocab_size=1000)
