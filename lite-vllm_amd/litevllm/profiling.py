@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import argparse
 import glob
+import re
 import sqlite3
 import statistics
 from pathlib import Path
@@ -124,7 +125,9 @@ def summarize_counters(pmc_dir: str) -> str:
     if cur:
         steps.append(cur)
     def is_prefix_pass(n: str) -> bool:
-        return "attn_chunk_mfma_kernel" in n and n.rstrip().endswith("true>")
+        # attn_chunk_mfma_kernel<T, D, G, BS, W, BPW, true> (names may carry
+        # the argument list after the template arguments)
+        return re.search(r"attn_chunk_mfma_kernel<[^<>]*,\s*true>", n) is not None
 
     def is_chunk(n: str) -> bool:
         return "attn_chunk_mfma_kernel" in n and not is_prefix_pass(n)
