@@ -566,9 +566,10 @@ class ModelRunner:
         """Host plan of the step's shared decode prefixes, or None."""
         cc = self.config.cache_config
         mc = self.model_config
-        if not cc.shared_prefix_attention or st.num_decodes < 2 or not \
-                ops.prefix_attention_supported(mc.num_attention_heads, mc.num_key_value_heads,
-                                               mc.head_dim, cc.block_size, mc.torch_dtype):
+        if not cc.shared_prefix_attention or not 2 <= st.num_decodes <= ops.PREFIX_MAX_DECODES:
+            return None
+        if not ops.prefix_attention_supported(mc.num_attention_heads, mc.num_key_value_heads,
+                                              mc.head_dim, cc.block_size, mc.torch_dtype):
             return None
         g = mc.num_attention_heads // mc.num_key_value_heads
         groups = find_shared_prefixes(st.descs, st.block_ids, st.num_decodes, cc.block_size, g)
