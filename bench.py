@@ -195,7 +195,7 @@ def bench_sampler(args):
         "ms_per_step": round(total_ms / args.steps, 4),
         "config": {"workload": "config4 fused sampler: [256, 151936] bf16 logits N(0,16), "
                                "rows 0-127 greedy, 128-255 T~U[0.5,1], supplied uniforms",
-                   "kernel": "lv_sample (sampler_kernel)"},
+                   "kernel": "lv_sample (sampler_segments_kernel + sampler_search_kernel)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": _traffic("sampler"),
