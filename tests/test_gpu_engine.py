@@ -205,6 +205,54 @@ def test_shared_prefix_attention_in_the_engine(device, monkeypatch):
     assert _compare_with_oracle(llm, prompts, outs, 20, 0.08, use_qk_norm=True) >= 6
 
 
+def test_decode_graph_replays_with_changing_prefix_plans(device, monkeypatch):
+    """Decode-graph replays while the shared-prefix plan changes from step to
+    step (sharers finish at different lengths, so groups shrink and the plan
+    empties): every replay equals the eager forward of the same static
+    buffers, plan included, and the plan was active in some replays and
+    empty in later ones."""
+    _say("decode graph replays with changing shared-prefix plans")
+    from litevllm.engine import model_runner as mr
+    monkeypatch.setattr(mr, "PREFIX_MIN_SAVED_BLOCKS", 1)
+    llm = LLM("tiny-qwen3", dtype="bfloat16", load_format="dummy", hf_overrides=QWEN3_SMALL,
+              skip_tokenizer_init=True, num_gpu_blocks=512, chunk_size=64,
+              enable_prefix_caching=True)
+    eng = llm.engine
+    runner = eng.model_runner
+    assert runner.graphs is not None and runner.graphs.use_prefix
+    orig = runner.execute_model
+    seen = []
+
+    def checked(meta):
+        logits = orig(meta)
+        if meta.graph_batch is not None:
+            b = meta.graph_batch
+            replayed = runner.graphs.logits[b].clone()
+            with torch.inference_mode():
+                eager = runner.graphs._forward(b)
+            torch.cuda.synchronize()
+            assert torch.equal(replayed, eager), f"replay {len(seen)}: batch {meta.num_decodes}"
+            seen.append(runner.graphs._pfx_active)
+        return logits
+
+    runner.execute_model = checked
+    g = torch.Generator().manual_seed(8)
+    shared = torch.randint(0, 5000, (96,), generator=g).tolist()
+    prompts = [shared + torch.randint(0, 5000, (5 + 7 * i,), generator=g).tolist()
+               for i in range(6)]
+    prompts += [torch.randint(0, 5000, (50,), generator=g).tolist() for _ in range(2)]
+    # the first prompt runs alone so its blocks are cached before the others
+    llm.generate(prompt_token_ids=prompts[:1],
+                 sampling_params=SamplingParams(temperature=0.0, max_tokens=2, ignore_eos=True))
+    for i, p in enumerate(prompts):
+        eng.add_request(None, SamplingParams(temperature=0.0, max_tokens=4 + 3 * i,
+                                             ignore_eos=True), prompt_token_ids=p)
+    outs = eng.run_to_completion()
+    assert sorted(o.num_output_tokens for o in outs) == [4 + 3 * i for i in range(len(prompts))]
+    assert eng.prefix_cache.hit_tokens >= 96
+    assert True in seen and False in seen[seen.index(True):], seen
+
+
 def test_sampling_with_temperature_is_seeded(device):
     _say("seeded temperature sampling")
     cfg = dict(TINY_LLAMA, vocab_size=1000)
