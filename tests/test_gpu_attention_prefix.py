@@ -150,6 +150,28 @@ def test_prefix_with_prefill_chunks(device):
     assert torch.equal(got[nd:].cpu(), plain[nd:].cpu())
 
 
+@pytest.mark.parametrize("dtype,heads", [(torch.bfloat16, (16, 8, 128)),
+                                         (torch.float16, (8, 8, 64)),
+                                         (torch.bfloat16, (32, 4, 128))])
+def test_prefix_interleaved_groups_and_leaders(device, dtype, heads):
+    """Groups whose rows interleave (even rows share one prefix, rows
+    1 mod 4 another), leaders that are not the group's first row, and
+    more members than one item slice holds: each member's query row is
+    found through prefix_members."""
+    H, Hkv, D = heads
+    _say(f"prefix interleaved groups {dtype} {heads}")
+    b = workloads.paged_decode(seed=12, num_seqs=200, num_heads=H, num_kv_heads=Hkv,
+                               head_dim=D, ctx_lo=400, ctx_hi=1800, dtype=dtype,
+                               scale_inputs=False)
+    even = list(range(0, 200, 2))
+    odd = list(range(1, 200, 4))
+    groups = [([even[37]] + even[:37] + even[38:], 20), ([odd[-1]] + odd[:-1], 9)]
+    b = _share(b, groups)
+    plan = ops.prefix_plan(groups, b.num_decodes, H // Hkv, device)
+    got = _run(b, device, plan)
+    _check(got, _oracle(b), f"interleaved {dtype} {heads}")
+
+
 def test_prefix_out_of_range_entries_are_skipped(device):
     """Items naming rows or splits outside their ranges do nothing (the rows
     of valid items are still right)."""
