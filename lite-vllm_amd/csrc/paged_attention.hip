@@ -584,6 +584,58 @@ __global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
     return;
   }
   const int per = a != b ? (total + num_wgs - 1) / num_wgs : 1;
+  if (g1 - g0 <= 1 && nsplit <= 4) {
+    // At most two pieces and four prefix splits (the common case): every
+    // value is loaded in one round trip, then merged in the order of the
+    // general loop below (same operations, same results).
+    const int np = g1 - g0 + 1;
+    float pm[2], pl[2], pa[2], qm[4], ql[4], qa[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      pm[i] = kNegBig; pl[i] = 0.0f; pa[i] = 0.0f;
+      if (i < np) {
+        const int g = g0 + i;
+        const int slot = (a <= g * per) ? 0 : 1;
+        const int64_t base = ((int64_t)g * 2 + slot) * num_heads + hq;
+        pm[i] = ws_ml[base * 2];
+        pl[i] = ws_ml[base * 2 + 1];
+        pa[i] = ws_acc[base * D + d];
+      }
+    }
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp) {
+      qm[sp] = kNegBig; ql[sp] = 0.0f; qa[sp] = 0.0f;
+      if (sp < nsplit) {
+        qm[sp] = pfx.ml[(pb + sp) * 2];
+        ql[sp] = pfx.ml[(pb + sp) * 2 + 1];
+        qa[sp] = pfx.acc[(pb + sp) * D + d];
+      }
+    }
+    float M = kNegBig;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (i < np) M = fmaxf(M, pm[i]);
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp)
+      if (sp < nsplit) M = fmaxf(M, qm[sp]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (i < np) {
+        const float f = pl[i] * fast_exp2(pm[i] - M);
+        L += f;
+        O = fmaf(pa[i], f, O);
+      }
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp)
+      if (sp < nsplit) {
+        const float f = ql[sp] * fast_exp2(qm[sp] - M);
+        L += f;
+        O = fmaf(qa[sp], f, O);
+      }
+    elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
+    return;
+  }
   float M = kNegBig;
   for (int g = g0; g <= g1; ++g) {
     const int slot = (a <= g * per) ? 0 : 1;
