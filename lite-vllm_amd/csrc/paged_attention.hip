@@ -438,6 +438,57 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
     if (whole && cur_skip > 0) {
       // fold in the prefix partials (splits of 128 keys), then normalise
       const int nsplit = (cur_skip * BS + kPrefixKeysPerSplit - 1) / kPrefixKeysPerSplit;
+      if constexpr (G <= 2) {
+        if (nsplit <= 4) {
+          // up to four splits: every partial is loaded in one round trip,
+          // then merged in the order of the general loop below
+          float qm[G][4], ql[G][4], qa[G][4][S::VEC];
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const int64_t pb = ((int64_t)sq * H + kvh * G + g) * kPrefixMaxSplits;
+#pragma unroll
+            for (int sp = 0; sp < 4; ++sp) {
+              qm[g][sp] = kNegBig;
+              ql[g][sp] = 0.0f;
+#pragma unroll
+              for (int j = 0; j < S::VEC; ++j) qa[g][sp][j] = 0.0f;
+              if (sp < nsplit) {
+                qm[g][sp] = pfx.ml[(pb + sp) * 2];
+                ql[g][sp] = pfx.ml[(pb + sp) * 2 + 1];
+                const float* ap = pfx.acc + (pb + sp) * D + st.dc * VEC;
+#pragma unroll
+                for (int j = 0; j < S::VEC; ++j) qa[g][sp][j] = ap[j];
+              }
+            }
+          }
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const int hq = kvh * G + g;
+            float mx = st.m[g];
+#pragma unroll
+            for (int sp = 0; sp < 4; ++sp)
+              if (sp < nsplit) mx = fmaxf(mx, qm[g][sp]);
+            const float fs = fast_exp2(st.m[g] - mx);
+            float L = st.l[g] * fs;
+            float o[S::VEC];
+#pragma unroll
+            for (int j = 0; j < S::VEC; ++j) o[j] = st.acc[g][j] * fs;
+#pragma unroll
+            for (int sp = 0; sp < 4; ++sp)
+              if (sp < nsplit) {
+                const float f = ql[g][sp] * fast_exp2(qm[g][sp] - mx);
+                L += f;
+#pragma unroll
+                for (int j = 0; j < S::VEC; ++j) o[j] = fmaf(qa[g][sp][j], f, o[j]);
+              }
+            const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+            T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + st.dc * VEC;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, o[j] * inv);
+          }
+          return;
+        }
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const int hq = kvh * G + g;
