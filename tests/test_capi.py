@@ -59,6 +59,37 @@ def test_host_side_argument_rejection():
                              _hip.LV_F32, None) == 0
 
 
+def test_prefix_entry_host_side_checks():
+    """lv_paged_attention_prefix rejects a bad plan description on the host
+    (nothing is dereferenced: the pointers below are never valid memory)."""
+    from litevllm import _hip
+    lib = _hip.load()
+    fake16, fake4 = 0x1000, 0x1004
+
+    def call(num_decodes=8, blocks=fake16, items=fake16, max_items=4, members=fake16,
+             pws=fake16, pws_bytes=1 << 30):
+        return lib.lv_paged_attention_prefix(
+            None, 0, None, None, 1, None, 1, None, None, num_decodes, num_decodes,
+            num_decodes, 1, 16, 8, 128, 16, 0.1, None, 0, None, 0,
+            blocks, items, max_items, members, pws, pws_bytes, _hip.LV_BF16, None)
+
+    assert call(num_decodes=0) == -1 and b"num_decodes" in lib.lv_last_error()
+    assert call(num_decodes=7001) == -1 and b"num_decodes" in lib.lv_last_error()
+    assert call(blocks=None) == -1 and b"null prefix" in lib.lv_last_error()
+    assert call(members=None) == -1 and b"null prefix" in lib.lv_last_error()
+    assert call(items=None) == -1 and b"null prefix" in lib.lv_last_error()
+    assert call(max_items=-1) == -1 and b"null prefix" in lib.lv_last_error()
+    assert call(items=fake4) == -1 and b"16-byte aligned" in lib.lv_last_error()
+    need = lib.lv_paged_attention_prefix_workspace_size(8, 16, 128)
+    assert call(pws_bytes=need - 1) == -3 and b"prefix workspace" in lib.lv_last_error()
+    assert call(pws=fake4) == -3
+    # (rows, heads, 16 splits) x ((m, l) + D floats), each part 256-byte aligned
+    n = 256 * 16 * 16
+    assert lib.lv_paged_attention_prefix_workspace_size(256, 16, 128) == \
+        -(-n * 2 * 4 // 256) * 256 + -(-n * 128 * 4 // 256) * 256
+    assert lib.lv_paged_attention_prefix_workspace_size(0, 16, 128) == 0
+
+
 def test_workspace_size_is_pure_host():
     from litevllm import _hip
     lib = _hip.load()
