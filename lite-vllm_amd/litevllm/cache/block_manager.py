@@ -85,6 +85,8 @@ class BlockManager:
         # Called with the number of blocks still missing; returns how many it
         # released.  Installed by the prefix cache when it is enabled.
         self.evictor: Optional[Callable[[int], int]] = None
+        # tables created by fork() (they share blocks with their source)
+        self.num_forks = 0
 
     @property
     def num_free_gpu_blocks(self) -> int:
@@ -136,4 +138,5 @@ class BlockManager:
             self.gpu_allocator.ref(block)
             dst.append(block)
         self.block_tables[dst_seq_id] = dst
+        self.num_forks += 1
         return dst

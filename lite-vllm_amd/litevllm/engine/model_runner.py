@@ -402,13 +402,13 @@ class DecodeGraphs:
                 and st.max_blocks <= self.max_blocks and bool(self.graphs))
 
     def prepare(self, st: StepDescriptors, staging: "_Staging",
-                device_tokens: Optional[torch.Tensor]) -> InputMetadata:
+                device_tokens: Optional[torch.Tensor], may_share: bool = True) -> InputMetadata:
         B = st.descs.shape[0]
         b = next(x for x in self.batches if x >= B)
         nb = st.block_ids.shape[0]
         n_host = len(st.tokens)
         groups = find_shared_prefixes(st.descs, st.block_ids, B, self.block_size,
-                                      self.group_size) if self.use_prefix else []
+                                      self.group_size) if self.use_prefix and may_share else []
         n_pfx = self.pfx_buf.numel() if (groups or self._pfx_active) else 0
         st32, st64 = staging.get(B * 6 + nb + n_pfx, max(n_host, 1))
         a32 = st32.numpy()
@@ -517,13 +517,14 @@ class ModelRunner:
         if st.uses_device_tokens and device_tokens is None:
             raise RuntimeError("a decode's last token is in flight but no device tokens were given")
         if self.graphs is not None and self.graphs.accepts(st):
-            return self.graphs.prepare(st, self._staging, device_tokens)
+            return self.graphs.prepare(st, self._staging, device_tokens,
+                                       self._may_share(block_manager))
         B, n_blocks = st.descs.shape[0], st.block_ids.shape[0]
         n_host, T = len(st.tokens), st.num_tokens
         h = max(n_host, 1)                   # keep the id array non-empty
         dev = torch.device(self.device)
         n32 = B * 6 + n_blocks
-        plan_arrays = self._prefix_arrays(st)
+        plan_arrays = self._prefix_arrays(st) if self._may_share(block_manager) else None
         p0 = (n32 + 3) // 4 * 4              # plan after the tables, 16-byte aligned
         n_all = p0 + sum(a.size for a in plan_arrays[:3]) + 4 if plan_arrays else n32
         st32, st64 = self._staging.get(n_all, h + len(st.logits_rows))
@@ -561,6 +562,12 @@ class ModelRunner:
                              num_decodes=st.num_decodes,
                              num_context_tokens=int(st.descs[:, 0].sum() + st.descs[:, 1].sum()),
                              num_context_blocks=int(n_blocks), prefix_stats=stats)
+
+    def _may_share(self, block_manager) -> bool:
+        """Whether block tables can share leading blocks: only prefix-cache
+        hits and forked tables do (otherwise the group search is skipped)."""
+        return (self.config.cache_config.enable_prefix_caching
+                or getattr(block_manager, "num_forks", 1) > 0)
 
     def _prefix_arrays(self, st: StepDescriptors):
         """Host plan of the step's shared decode prefixes, or None."""

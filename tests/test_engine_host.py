@@ -38,7 +38,9 @@ def test_can_allocate_append_fork_and_exhaustion():
     bm.allocate(1, 1)
     bm.append_slot(1)
     assert len(bm.get_block_table(1)) == 2 and bm.num_free_gpu_blocks == 2
+    assert bm.num_forks == 0
     bm.fork(1, 2)
+    assert bm.num_forks == 1   # the runner's shared-prefix search looks for sharing again
     assert all(b.ref_count == 2 for b in bm.get_block_table(1).blocks)
     bm.free(1)
     assert bm.num_free_gpu_blocks == 2
