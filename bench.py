@@ -338,6 +338,7 @@ def bench_e2e(args):
     hits0 = eng.prefix_cache.hit_tokens
     t0 = time.perf_counter()
     n_out = 0
+    outs = []
     for i in range(args.steps):
         outs = llm.generate(prompt_token_ids=prompts, sampling_params=sp)
         n_out += sum(o.num_output_tokens for o in outs)
@@ -352,6 +353,8 @@ def bench_e2e(args):
     mr.DecodeGraphs.accepts = orig_accepts
     durs = [a.elapsed_time(b) for a, b in probe["durs"]]
     cpu_state = cpu_cfg = None
+    by_prompt = {tuple(o.prompt_token_ids): list(o.output_token_ids) for o in outs}
+    streams = [by_prompt[tuple(p)] for p in prompts[:8]]
     if not args.no_cpu_baseline:
         cpu_state = {k: v.detach().to("cpu", torch.float32)
                      for k, v in eng.model_runner.model.state_dict().items()}
@@ -395,7 +398,8 @@ def bench_e2e(args):
     torch.cuda.empty_cache()
     if args.no_secondary:
         if not args.no_cpu_baseline:
-            result["cpu_baseline"] = cpu_baseline_e2e(cpu_state, cpu_cfg, prompts)
+            result["cpu_baseline"], result["parity"] = cpu_baseline_e2e(
+                cpu_state, cpu_cfg, prompts, streams)
         return result
     _log("e2e: config-2 decode-attention microbench")
     dec = bench_decode(argparse.Namespace(steps=50, warmup=10, no_cpu_baseline=True))
@@ -404,38 +408,72 @@ def bench_e2e(args):
         "value": dec["value"], "unit": dec["unit"], "roofline": dec["roofline"],
         "config": dec["config"]["workload"]}
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_e2e(cpu_state, cpu_cfg, prompts)
+        result["cpu_baseline"], result["parity"] = cpu_baseline_e2e(
+            cpu_state, cpu_cfg, prompts, streams)
     return result
 
 
-def cpu_baseline_e2e(state, model_config, prompts, n_seqs: int = 8, n_steps: int = 4):
+def cpu_baseline_e2e(state, model_config, prompts, streams, n_seqs: int = 8, n_steps: int = 4,
+                     margin_bar: float = 0.1):
     """The reference's CPU model path restated (oracle.model, fp32, the same
     random weights): prefill the first n_seqs prompts of the workload
-    (untimed), then time n_steps batched greedy decode steps."""
+    (untimed), then time n_steps batched greedy decode steps.
+
+    The decode steps are fed the engine's own tokens for those prompts
+    (``streams``, from the timed run), so the same pass also checks them:
+    each of the first n_steps + 1 engine tokens must be the oracle's argmax
+    where the oracle's top-2 margin is at least margin_bar, and within
+    margin_bar of the oracle's maximum everywhere (the bf16 bar of the
+    config-5 GPU test).  Returns (cpu_baseline, parity)."""
     import torch
     from oracle.model import OracleDecoder
     threads = _cpu_threads()
     torch.set_num_threads(threads)
     o = OracleDecoder(state, model_config, use_qk_norm=True)
-    kvs, toks, pos = [], [], []
+    n_steps = max(0, min(n_steps, min(len(s) for s in streams[:n_seqs]) - 1))
+    checked = exact = 0
+    max_gap = 0.0
+
+    def check(logits, t):
+        nonlocal checked, exact, max_gap
+        top2 = torch.topk(logits, 2, dim=-1).values
+        for r in range(logits.shape[0]):
+            tok = streams[r][t]
+            gap = float(top2[r, 0] - logits[r, tok])
+            max_gap = max(max_gap, gap)
+            if float(top2[r, 0] - top2[r, 1]) >= margin_bar:
+                exact += int(tok == int(torch.argmax(logits[r])))
+                checked += 1
+
+    kvs, first, pos = [], [], []
     for p in prompts[:n_seqs]:
         kv: list = []
-        toks.append(int(torch.argmax(o.forward(p, 0, kv))))
+        first.append(o.forward(p, 0, kv))
         kvs.append(kv)
         pos.append(len(p))
+    check(torch.stack(first), 0)
     _log("e2e cpu baseline: prefill done")
-    t0 = time.perf_counter()
-    for _ in range(n_steps):
-        logits = o.decode_batch(toks, pos, kvs)
-        toks = logits.argmax(-1).tolist()
+    secs = 0.0
+    for t in range(n_steps):
+        t0 = time.perf_counter()
+        logits = o.decode_batch([s[t] for s in streams[:n_seqs]], pos, kvs)
+        secs += time.perf_counter() - t0
+        check(logits, t + 1)
         pos = [x + 1 for x in pos]
-    secs = time.perf_counter() - t0
-    return {"value": round(n_seqs * n_steps / secs, 2), "unit": "output tok/s",
+    base = {"value": round(n_seqs * n_steps / max(secs, 1e-9), 2), "unit": "output tok/s",
             "cores": threads, "kind": "port",
             "sample": f"config5 prompts 0..{n_seqs - 1} ({sum(map(len, prompts[:n_seqs]))} prompt "
                       f"tokens, prefill untimed), {n_steps} batched greedy decode steps of "
                       f"oracle.model.OracleDecoder (fp32 restatement of the reference model "
                       f"path): {secs:.2f} s"}
+    parity = {"rows": n_seqs, "tokens_per_row": n_steps + 1,
+              "clear_margin_tokens": checked, "argmax_match": exact,
+              "max_gap_below_oracle_max": round(max_gap, 4), "bar": margin_bar,
+              "ok": exact == checked and max_gap <= margin_bar,
+              "check": "engine tokens of the timed run (prompts 0-7, first 5 tokens) vs the fp32 "
+                       "oracle decoder teacher-forced on them: argmax where the oracle's top-2 "
+                       "margin >= bar, within bar of its max everywhere"}
+    return base, parity
 
 
 def bench_copy(args):
@@ -499,7 +537,7 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded torch.Generator, seed 0)", "config": res["config"],
     }
-    for k in ("roofline", "cpu_baseline", "secondary"):
+    for k in ("roofline", "cpu_baseline", "parity", "secondary"):
         if k in res:
             line[k] = res[k]
     print(json.dumps(line), flush=True)

@@ -75,7 +75,7 @@ def _groups_for(ctx: torch.Tensor, spans, bs=16):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("heads", [(16, 8, 128), (4, 2, 64), (8, 8, 128), (32, 4, 64),
-                                   (16, 2, 128)])
+                                   (16, 2, 128), (32, 8, 128), (16, 4, 64)])
 def test_prefix_shapes(device, dtype, heads):
     H, Hkv, D = heads
     _say(f"prefix shapes dtype={dtype} H={H} Hkv={Hkv} D={D}")

@@ -120,7 +120,8 @@ def _oracle(batch: workloads.PagedBatch):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("heads", [(16, 8, 128), (4, 2, 64), (8, 8, 128), (32, 4, 64), (16, 2, 128)])
+@pytest.mark.parametrize("heads", [(16, 8, 128), (4, 2, 64), (8, 8, 128), (32, 4, 64),
+                                   (16, 2, 128), (32, 8, 128), (16, 4, 64)])
 def test_decode_small_shapes(device, dtype, heads):
     H, Hkv, D = heads
     _say(f"decode small dtype={dtype} H={H} Hkv={Hkv} D={D}")
@@ -172,7 +173,8 @@ def test_mixed_step_small(device, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("heads", [(16, 8, 128), (4, 2, 64), (8, 8, 128), (32, 4, 64), (16, 2, 128)])
+@pytest.mark.parametrize("heads", [(16, 8, 128), (4, 2, 64), (8, 8, 128), (32, 4, 64),
+                                   (16, 2, 128), (32, 8, 128), (16, 4, 64)])
 def test_chunks_all_shapes(device, dtype, heads):
     """Prefill chunks at unaligned offsets (MFMA path for bf16/fp16, per-row
     path for fp32), mixed with decodes, against the fp32 oracle."""
