@@ -22,7 +22,8 @@ QWEN3_TINY = dict(model_type="qwen3", vocab_size=512, hidden_size=128, num_hidde
                   num_attention_heads=4, num_key_value_heads=2, head_dim=64,
                   intermediate_size=256, rope_theta=1e6, rms_norm_eps=1e-6,
                   max_position_embeddings=1024, tie_word_embeddings=False)
-LLAMA_TINY = dict(model_type="llama", vocab_size=512, hidden_size=128, num_hidden_layers=2,
+# head_dim = hidden / heads = 64 (the attention kernels take head_dim 64 or 128)
+LLAMA_TINY = dict(model_type="llama", vocab_size=512, hidden_size=256, num_hidden_layers=2,
                   num_attention_heads=4, num_key_value_heads=2, intermediate_size=320,
                   rope_theta=10000.0, rms_norm_eps=1e-5, max_position_embeddings=1024,
                   tie_word_embeddings=False)
