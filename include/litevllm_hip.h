@@ -265,6 +265,23 @@ int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
               const float* uniform_dev, int64_t* out_ids_dev, void* workspace_dev,
               size_t workspace_bytes, lv_dtype dtype, void* stream);
 
+/* lv_sample without a workspace argument: it allocates nothing (no
+ * hipMalloc / hipFree, no allocating library call).  No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * Arguments, results and errors are those of lv_sample.  Its scratch is a
+ * fixed 4 MiB array in the library's device code, one copy per GPU, looked
+ * up on the first call on each device; calls needing more than
+ * lv_sample_workspace_size(num_rows, vocab_size) <= 4 MiB (e.g. above 1564
+ * rows at vocab 151936) are rejected with LV_ERR_WORKSPACE.  Every call on a
+ * GPU uses that GPU's one copy: calls that overlap on one GPU (two streams,
+ * two threads) race.
+ */
+int lv_sample_noalloc(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
+                      int64_t row_stride, const float* temperature_dev,
+                      const float* uniform_dev, int64_t* out_ids_dev, lv_dtype dtype,
+                      void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused layer prologue / epilogue work (the elementwise ops the reference
  * runs as separate torch ops around its GEMMs).  Rounding follows the

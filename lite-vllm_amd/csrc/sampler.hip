@@ -45,6 +45,9 @@
 // fmaf, rint and exact power-of-two scaling.
 #include <stdlib.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "lv_common.h"
 
 namespace lv {
@@ -398,35 +401,21 @@ extern "C" size_t lv_sample_workspace_size(int64_t num_rows, int64_t vocab_size)
   return samp_ws_bytes(num_rows, vocab_size);
 }
 
-extern "C" int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
-                         int64_t row_stride, const float* temperature_dev, const float* uniform_dev,
-                         int64_t* out_ids_dev, void* workspace_dev, size_t workspace_bytes,
-                         lv_dtype dtype, void* stream) {
-  using namespace lv;
-  clear_error();
-  LV_REQUIRE(dtype == LV_F32 || dtype == LV_F16 || dtype == LV_BF16, "lv_sample: bad dtype");
-  LV_REQUIRE(num_rows >= 0 && num_rows <= 0x7fffffff, "lv_sample: bad num_rows");
-  if (num_rows == 0) return LV_OK;
-  LV_REQUIRE(vocab_size >= 1 && vocab_size <= (int64_t)kSeg * kMaxSegs,
-             "lv_sample: vocab_size=%lld outside [1, %d]", (long long)vocab_size, kSeg * kMaxSegs);
-  LV_REQUIRE(row_stride >= vocab_size, "lv_sample: row_stride < vocab_size");
-  LV_REQUIRE(logits_dev && temperature_dev && out_ids_dev, "lv_sample: null pointer");
-  LV_REQUIRE(uniform_dev, "lv_sample: uniform draws required (pass zeros for all-greedy rows)");
-  const size_t need = samp_ws_bytes(num_rows, vocab_size);
-  if (!workspace_dev || workspace_bytes < need) {
-    set_error("lv_sample: workspace of %zu bytes required, got %zu", need, workspace_bytes);
-    return LV_ERR_WORKSPACE;
-  }
+namespace lv {
+// Enqueue both kernels with the workspace at `base` (256-byte aligned, at
+// least samp_ws_bytes(num_rows, vocab_size) - 256 bytes).
+static int sample_launch(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
+                         int64_t row_stride, const float* temperature_dev,
+                         const float* uniform_dev, int64_t* out_ids_dev, char* base,
+                         lv_dtype dtype, hipStream_t st) {
   const int vec = aligned16(logits_dev) && ((row_stride * (int64_t)dtype_size(dtype)) % 16 == 0);
   const int nseg = (int)((vocab_size + kSeg - 1) / kSeg);
   const int split = (int)samp_split(nseg);
-  char* base = (char*)(((uintptr_t)workspace_dev + 255) & ~(uintptr_t)255);
   SampWs ws;
   ws.bi = (int64_t*)base;
   ws.bv = (float*)(base + (size_t)num_rows * split * 8);
   ws.m = (float*)(base + (size_t)num_rows * split * 12);
   ws.w = ws.m + (size_t)num_rows * nseg;
-  hipStream_t st = (hipStream_t)stream;
   const dim3 grid_a((unsigned)num_rows, (unsigned)split), grid_b((unsigned)num_rows);
   const dim3 block(kSegThreads);
 #define LV_SEG(TT, U, G)                                                                        \
@@ -451,4 +440,100 @@ extern "C" int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab
 #undef LV_SAMPLE_LAUNCH
 #undef LV_SEG
   return check_launch("sampler kernels");
+}
+
+// Argument checks shared by both entry points.
+static int sample_check(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
+                        int64_t row_stride, const float* temperature_dev,
+                        const float* uniform_dev, const int64_t* out_ids_dev, lv_dtype dtype) {
+  LV_REQUIRE(dtype == LV_F32 || dtype == LV_F16 || dtype == LV_BF16, "lv_sample: bad dtype");
+  LV_REQUIRE(num_rows >= 0 && num_rows <= 0x7fffffff, "lv_sample: bad num_rows");
+  if (num_rows == 0) return LV_OK;
+  LV_REQUIRE(vocab_size >= 1 && vocab_size <= (int64_t)kSeg * kMaxSegs,
+             "lv_sample: vocab_size=%lld outside [1, %d]", (long long)vocab_size, kSeg * kMaxSegs);
+  LV_REQUIRE(row_stride >= vocab_size, "lv_sample: row_stride < vocab_size");
+  LV_REQUIRE(logits_dev && temperature_dev && out_ids_dev, "lv_sample: null pointer");
+  LV_REQUIRE(uniform_dev, "lv_sample: uniform draws required (pass zeros for all-greedy rows)");
+  return LV_OK;
+}
+
+// Scratch of lv_sample_noalloc: one copy per GPU in the code object's own
+// device memory, so that entry point never allocates.  Host code must use
+// the per-device address returned by hipGetSymbolAddress (scratch_device_ptr),
+// never the array's name, which on the host is only a stand-in.  Every call
+// on a GPU shares that GPU's copy; nothing in it needs to start at zero
+// (each call writes every entry it reads before reading it).
+constexpr size_t kSampleScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) char scratch[kSampleScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch (looked up once per
+// device, with that device current); nullptr with the error set on failure.
+static void* scratch_device_ptr() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("lv_sample_noalloc: no current HIP device (or device id >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+  if (p == nullptr) {
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("lv_sample_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+}  // namespace lv
+
+extern "C" int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
+                         int64_t row_stride, const float* temperature_dev, const float* uniform_dev,
+                         int64_t* out_ids_dev, void* workspace_dev, size_t workspace_bytes,
+                         lv_dtype dtype, void* stream) {
+  using namespace lv;
+  clear_error();
+  const int rc = sample_check(logits_dev, num_rows, vocab_size, row_stride, temperature_dev,
+                              uniform_dev, out_ids_dev, dtype);
+  if (rc != LV_OK || num_rows == 0) return rc;
+  const size_t need = samp_ws_bytes(num_rows, vocab_size);
+  if (!workspace_dev || workspace_bytes < need) {
+    set_error("lv_sample: workspace of %zu bytes required, got %zu", need, workspace_bytes);
+    return LV_ERR_WORKSPACE;
+  }
+  char* base = (char*)(((uintptr_t)workspace_dev + 255) & ~(uintptr_t)255);
+  return sample_launch(logits_dev, num_rows, vocab_size, row_stride, temperature_dev, uniform_dev,
+                       out_ids_dev, base, dtype, (hipStream_t)stream);
+}
+
+extern "C" int lv_sample_noalloc(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
+                                 int64_t row_stride, const float* temperature_dev,
+                                 const float* uniform_dev, int64_t* out_ids_dev, lv_dtype dtype,
+                                 void* stream) {
+  using namespace lv;
+  clear_error();
+  const int rc = sample_check(logits_dev, num_rows, vocab_size, row_stride, temperature_dev,
+                              uniform_dev, out_ids_dev, dtype);
+  if (rc != LV_OK || num_rows == 0) return rc;
+  // samp_ws_bytes includes 256 bytes of alignment slack the scratch does not
+  // need; the bound below is the documented one (lv_sample_workspace_size).
+  const size_t need = samp_ws_bytes(num_rows, vocab_size);
+  if (need > kSampleScratchBytes) {
+    set_error("lv_sample_noalloc: %lld rows x vocab %lld need %zu bytes of scratch, above the "
+              "fixed %zu (use lv_sample with a workspace)", (long long)num_rows,
+              (long long)vocab_size, need, kSampleScratchBytes);
+    return LV_ERR_WORKSPACE;
+  }
+  char* base = (char*)scratch_device_ptr();
+  if (base == nullptr) return LV_ERR_HIP;
+  return sample_launch(logits_dev, num_rows, vocab_size, row_stride, temperature_dev, uniform_dev,
+                       out_ids_dev, base, dtype, (hipStream_t)stream);
 }

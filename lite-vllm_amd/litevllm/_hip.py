@@ -83,6 +83,11 @@ SIGNATURES: dict[str, tuple] = {
         _c_p, ctypes.c_size_t,         # workspace, workspace_bytes
         ctypes.c_int, _c_p,            # dtype, stream
     ]),
+    "lv_sample_noalloc": (ctypes.c_int, [
+        _c_p, _c_i64, _c_i64, _c_i64,  # logits, num_rows, vocab_size, row_stride
+        _c_p, _c_p, _c_p,              # temperature, uniform, out_ids
+        ctypes.c_int, _c_p,            # dtype, stream
+    ]),
     "lv_add_rms_norm": (ctypes.c_int, [
         _c_p, _c_i64, _c_p, _c_i64,    # x, x_stride, residual, residual_stride
         _c_p, _c_p, _c_i64,            # weight, out, out_stride

@@ -123,3 +123,20 @@ def test_sampler_workspace_size_and_rejection():
     # that are never dereferenced on the host)
     rc = lib.lv_sample(1, 4, 1000, 1000, 1, 1, 1, 1, 8, _hip.LV_BF16, None)
     assert rc == -3 and b"workspace" in lib.lv_last_error()
+
+
+def test_sample_noalloc_refuses_requests_beyond_its_scratch():
+    """lv_sample_noalloc's scratch is a fixed 4 MiB: a request needing more
+    is refused on the host, before any device call (none is possible here:
+    this check runs without a GPU)."""
+    from litevllm import _hip
+    lib = _hip.load()
+    p = ctypes.c_void_p(256)      # never dereferenced: the size check comes first
+    need = int(lib.lv_sample_workspace_size(4096, 151936))
+    assert need > 4 << 20
+    rc = lib.lv_sample_noalloc(p, 4096, 151936, 151936, p, p, p, _hip.LV_BF16, None)
+    assert rc == -3 and b"scratch" in lib.lv_last_error()
+    assert int(lib.lv_sample_workspace_size(1564, 151936)) <= 4 << 20
+    assert int(lib.lv_sample_workspace_size(1566, 151936)) > 4 << 20
+    rc = lib.lv_sample_noalloc(None, 4, 100, 100, None, None, None, _hip.LV_BF16, None)
+    assert rc == -1 and b"null pointer" in lib.lv_last_error()
