@@ -51,7 +51,7 @@ const char* lv_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int lv_abi_version(void);
-#define LV_ABI_VERSION 5
+#define LV_ABI_VERSION 6
 
 /* ------------------------------------------------------------------------
  * (1) Ragged-batch packing.
@@ -195,19 +195,19 @@ int lv_paged_attention(const void* query_dev, int64_t q_stride_t,
  * prefix_blocks: int32 [num_decodes], leading blocks of row i attended by
  * the prefix pass (0 = none); for a member of a group it is the group's
  * prefix length, at most 128 blocks, and prefix_blocks[i] * block_size <=
- * context_lens[i].  prefix_members: int32, the member rows of each group
- * listed together.  prefix_items: int32 [max_items][4], 16-byte aligned,
- * (may be NULL when max_items is 0),
- * one work item per (group, slice of up to 128 / G members, 128-key split
- * of the prefix): {leader row, index of the slice's first member in
+ * context_lens[i].  prefix_members: int32 [num_members], the member rows of
+ * each group listed together.  prefix_items: int32 [max_items][4], 16-byte
+ * aligned (may be NULL when max_items is 0): one work item per (group,
+ * slice of up to 128 / G members, 128-key split of the prefix): {leader row, index of the slice's first member in
  * prefix_members, members in the slice, split}; leader row < 0 marks an
  * unused item.  Every member's prefix rows must be covered by exactly one
  * item per split, and the first prefix_blocks[leader] entries of every
- * member's block table must equal the leader's (the pass reads the leader's
- * table).  A slice holds at most 128 / G members (more are not read).
- * Leader and member rows outside [0, num_decodes) and splits outside
- * [0, 16) are skipped; every index an item names into prefix_members must
- * lie inside it.
+ * member's block table must equal the leader's (the pass reads the
+ * leader's table).  Items are skipped when their leader is outside
+ * [0, num_decodes), their split outside [0, 16), their slice empty, wider
+ * than 128 / G members or outside prefix_members [0, num_members); member
+ * rows outside [0, num_decodes) are skipped.  (litevllm.ops.
+ * prefix_plan_arrays builds and checks such arrays on the host.)
  * prefix_workspace: at least lv_paged_attention_prefix_workspace_size(...)
  * bytes, 256-B aligned, contents need not be initialised; one per stream.
  * Supported: bf16 / fp16, head_dim 64 / 128, block_size 16, G in
@@ -232,7 +232,7 @@ int lv_paged_attention_prefix(const void* query_dev, int64_t q_stride_t,
                               void* workspace_dev, size_t workspace_bytes,
                               const int32_t* prefix_blocks_dev,
                               const int32_t* prefix_items_dev, int32_t max_items,
-                              const int32_t* prefix_members_dev,
+                              const int32_t* prefix_members_dev, int32_t num_members,
                               void* prefix_workspace_dev, size_t prefix_workspace_bytes,
                               lv_dtype dtype, void* stream);
 

@@ -26,6 +26,7 @@
 
 #include "lv_common.h"
 #include "lv_mfma.h"
+#include "lv_split.h"
 
 namespace lv {
 
@@ -318,15 +319,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(
 // Shared-prefix (cascade) pass.  Decode sequences whose block tables begin
 // with the same physical blocks (prefix-cache hits) form a group; the
 // group's first P blocks are attended once for all members by the MFMA
-// kernel in prefix mode, and the decode kernel only walks each member's
-// remaining blocks and merges the prefix partials in.  Prefix partials are
-// indexed [row][query head][split] (split = 128-key slice of the prefix) and
-// hold (m, l) in log2 units and acc normalised by l.
+// body in prefix mode (a launch before the decode kernel), and the decode
+// kernel only walks each member's remaining blocks and merges the prefix
+// partials in.  Prefix partials are indexed [row][query head][split]
+// (split = 128-key slice of the prefix) and hold (m, l) in log2 units and
+// acc normalised by l.
 struct PrefixArgs {
-  const int32_t* blocks;   // [num_decodes] leading blocks handled by the prefix pass (0 = none)
+  const int32_t* blocks;   // [num_decodes] leading blocks handled by the prefix units (0 = none)
   const int32_t* items;    // [max_items][4]: leader row, first member, member count, split
   const int32_t* members;  // member rows, grouped
   int max_items;
+  int num_members;         // entries of `members`
   float* ml;               // [rows][H][kPrefixMaxSplits][2]
   float* acc;              // [rows][H][kPrefixMaxSplits][D]
 };
@@ -334,6 +337,7 @@ constexpr int kPrefixKeysPerSplit = 128;
 constexpr int kPrefixMaxSplits = 16;   // prefixes up to 2048 tokens
 constexpr int kPrefixMaxBlocks = kPrefixKeysPerSplit * kPrefixMaxSplits / 16;
 constexpr int kPrefixMaxRows = 7000;   // decode rows: offsets + skips stay in 56 KB of LDS
+
 
 constexpr int kPersistMaxWaves = 8;  // kv heads per workgroup (one wavefront each)
 constexpr int kPersistMaxSeqs = 15000;  // (B+1) ints of LDS stay under 60 KB
@@ -378,335 +382,6 @@ __device__ void scan_block_counts(const int32_t* __restrict__ ctx,
   }
   if (t == nt - 1) s_off[n] = s_part[nt - 1];
   __syncthreads();
-}
-
-template <typename T, int D, int G, int BS, bool NT, int NBUF>
-__global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_kernel(
-    const T* __restrict__ q, int64_t q_stride,
-    const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
-    const int32_t* __restrict__ block_tables, int max_blocks, const int32_t* __restrict__ ctx,
-    int num_seqs, float scale_log2, T* __restrict__ out, int64_t out_stride,
-    int32_t* __restrict__ ws_off, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
-    PrefixArgs pfx) {
-  using S = HeadState<T, D, G, BS, NT>;
-  constexpr int VEC = S::VEC;
-  // LDS: s_off [num_seqs + 1], then (shared-prefix pass only) s_skip [num_seqs]
-  extern __shared__ int32_t s_off[];
-  int32_t* s_skip = s_off + num_seqs + 1;
-  __shared__ int32_t s_part[kPersistMaxWaves * 64];
-  const int max_tokens = max_blocks * BS;
-  const bool has_pfx = pfx.blocks != nullptr;
-  scan_block_counts<BS>(ctx, pfx.blocks, num_seqs, max_tokens, s_off, s_part, s_skip);
-  const int total = s_off[num_seqs];
-  const int H = num_kv_heads * G;
-  // ws_off: offsets [num_seqs + 1], then each sequence's skipped blocks
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i <= num_seqs; i += blockDim.x) {
-      ws_off[i] = s_off[i];
-      if (has_pfx && i < num_seqs) ws_off[num_seqs + 1 + i] = s_skip[i];
-    }
-  if (total == 0) return;
-  const int per = (total + gridDim.x - 1) / gridDim.x;
-  const int r0 = blockIdx.x * per;
-  const int r1 = min(total, r0 + per);
-  if (r0 >= r1) return;
-
-  const int lane = threadIdx.x & 63;
-  const int kvh = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (kvh >= num_kv_heads) return;
-  const int64_t tok_stride = (int64_t)num_kv_heads * D;
-  const int64_t blk_stride = (int64_t)BS * tok_stride;
-
-  S st;
-  st.tg = lane / S::RL;
-  st.dc = lane % S::RL;
-  const int64_t lane_off = (int64_t)kvh * D + st.dc * VEC + st.tg * tok_stride;
-  const T* kbase = kc + lane_off;
-  const T* vbase = vc + lane_off;
-
-  int cur = -1;     // sequence whose state st holds (uniform)
-  int cur_end = 0;  // its context length
-  int cur_skip = 0; // its leading blocks attended by the shared-prefix pass
-
-  // Finish sequence sq: a piece covering the whole sequence goes straight to
-  // `out`, any other piece to this workgroup's slot 0 (first piece) or 1.
-  auto finish = [&](int sq) __attribute__((always_inline)) {
-    st.merge_token_groups();
-    const int a = s_off[sq], b = s_off[sq + 1];
-    const bool whole = a >= r0 && b <= r1;
-    if (st.tg != 0) return;
-    if (whole && cur_skip > 0) {
-      // fold in the prefix partials (splits of 128 keys), then normalise
-      const int nsplit = (cur_skip * BS + kPrefixKeysPerSplit - 1) / kPrefixKeysPerSplit;
-      if constexpr (G <= 2) {
-        if (nsplit <= 4) {
-          // up to four splits: every partial is loaded in one round trip,
-          // then merged in the order of the general loop below
-          float qm[G][4], ql[G][4], qa[G][4][S::VEC];
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const int64_t pb = ((int64_t)sq * H + kvh * G + g) * kPrefixMaxSplits;
-#pragma unroll
-            for (int sp = 0; sp < 4; ++sp) {
-              qm[g][sp] = kNegBig;
-              ql[g][sp] = 0.0f;
-#pragma unroll
-              for (int j = 0; j < S::VEC; ++j) qa[g][sp][j] = 0.0f;
-              if (sp < nsplit) {
-                qm[g][sp] = pfx.ml[(pb + sp) * 2];
-                ql[g][sp] = pfx.ml[(pb + sp) * 2 + 1];
-                const float* ap = pfx.acc + (pb + sp) * D + st.dc * VEC;
-#pragma unroll
-                for (int j = 0; j < S::VEC; ++j) qa[g][sp][j] = ap[j];
-              }
-            }
-          }
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const int hq = kvh * G + g;
-            float mx = st.m[g];
-#pragma unroll
-            for (int sp = 0; sp < 4; ++sp)
-              if (sp < nsplit) mx = fmaxf(mx, qm[g][sp]);
-            const float fs = fast_exp2(st.m[g] - mx);
-            float L = st.l[g] * fs;
-            float o[S::VEC];
-#pragma unroll
-            for (int j = 0; j < S::VEC; ++j) o[j] = st.acc[g][j] * fs;
-#pragma unroll
-            for (int sp = 0; sp < 4; ++sp)
-              if (sp < nsplit) {
-                const float f = ql[g][sp] * fast_exp2(qm[g][sp] - mx);
-                L += f;
-#pragma unroll
-                for (int j = 0; j < S::VEC; ++j) o[j] = fmaf(qa[g][sp][j], f, o[j]);
-              }
-            const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-            T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + st.dc * VEC;
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, o[j] * inv);
-          }
-          return;
-        }
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const int hq = kvh * G + g;
-        const int64_t pb = ((int64_t)sq * H + hq) * kPrefixMaxSplits;
-        float mx = st.m[g];
-        for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, pfx.ml[(pb + sp) * 2]);
-        const float fs = fast_exp2(st.m[g] - mx);
-        float L = st.l[g] * fs;
-        float o[S::VEC];
-#pragma unroll
-        for (int j = 0; j < S::VEC; ++j) o[j] = st.acc[g][j] * fs;
-        for (int sp = 0; sp < nsplit; ++sp) {
-          const float f = pfx.ml[(pb + sp) * 2 + 1] * fast_exp2(pfx.ml[(pb + sp) * 2] - mx);
-          L += f;
-          const float* ap = pfx.acc + (pb + sp) * D + st.dc * VEC;
-#pragma unroll
-          for (int j = 0; j < S::VEC; ++j) o[j] = fmaf(ap[j], f, o[j]);
-        }
-        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-        T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + st.dc * VEC;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, o[j] * inv);
-      }
-      return;
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int hq = kvh * G + g;
-      const float inv = st.l[g] > 0.0f ? 1.0f / st.l[g] : 0.0f;
-      if (whole) {
-        T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + st.dc * VEC;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, st.acc[g][j] * inv);
-      } else {
-        const int slot = (a <= r0) ? 0 : 1;
-        const int64_t base = ((int64_t)blockIdx.x * 2 + slot) * H + hq;
-        float* wp = ws_acc + base * D + st.dc * VEC;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) wp[j] = st.acc[g][j] * inv;
-        if (st.dc == 0) { ws_ml[base * 2] = st.m[g]; ws_ml[base * 2 + 1] = st.l[g]; }
-      }
-    }
-  };
-
-  static_assert(NBUF == 2 || NBUF == 4, "NBUF");
-  uint4 k0[S::LOADS], v0[S::LOADS], k1[S::LOADS], v1[S::LOADS];
-  uint4 k2[NBUF == 4 ? S::LOADS : 1], v2[NBUF == 4 ? S::LOADS : 1];
-  uint4 k3[NBUF == 4 ? S::LOADS : 1], v3[NBUF == 4 ? S::LOADS : 1];
-  for (int base = r0; base < r1; base += 64) {
-    const int cnt = min(64, r1 - base);
-    // Lane i resolves flattened entry base + i: its sequence, logical block
-    // and physical block id.
-    int lseq = 0, lblk = 0, id = 0;
-    if (lane < cnt) {
-      const int j = base + lane;
-      int lo = 0, hi = num_seqs - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s_off[mid] <= j) lo = mid; else hi = mid - 1;
-      }
-      lseq = lo;
-      lblk = j - s_off[lo] + (has_pfx ? s_skip[lo] : 0);   // block index in the table
-      id = block_tables[(int64_t)lo * max_blocks + lblk];
-    }
-    if (id < 0 || id >= num_cache_blocks) id = 0;
-    auto phys = [&](int i) { return __builtin_amdgcn_readlane(id, min(i, cnt - 1)); };
-    // Start (or continue) the sequence of entry i, then fold its block in;
-    // i >= cnt is a fully masked no-op so process() always runs.
-    auto visit = [&](const uint4* kk, const uint4* vv, int i) {
-      const bool real = i < cnt;
-      const int sq = __builtin_amdgcn_readlane(lseq, min(i, cnt - 1));
-      const int lb = __builtin_amdgcn_readlane(lblk, min(i, cnt - 1));
-      if (real && sq != cur) {
-        if (cur >= 0) finish(cur);
-        cur = sq;
-        cur_end = min(max(ctx[sq], 0), max_tokens);
-        cur_skip = has_pfx ? s_skip[sq] : 0;
-        st.init(q + (int64_t)sq * q_stride + (int64_t)kvh * G * D, scale_log2, lane);
-      }
-      st.process(kk, vv, lb, real ? cur_end : -1);
-    };
-    // NBUF register buffers rotate: NBUF - 1 blocks are in flight while one
-    // is folded in.  Loads past the group end reload its last block (cache
-    // hit) and their visits are masked no-ops.
-    if constexpr (NBUF == 2) {
-      st.load(kbase, vbase, phys(0), blk_stride, tok_stride, k0, v0);
-      for (int i = 0; i < cnt; i += 2) {
-        st.load(kbase, vbase, phys(i + 1), blk_stride, tok_stride, k1, v1);
-        __builtin_amdgcn_sched_barrier(0);
-        visit(k0, v0, i);
-        st.load(kbase, vbase, phys(i + 2), blk_stride, tok_stride, k0, v0);
-        __builtin_amdgcn_sched_barrier(0);
-        visit(k1, v1, i + 1);
-      }
-    } else {
-      st.load(kbase, vbase, phys(0), blk_stride, tok_stride, k0, v0);
-      st.load(kbase, vbase, phys(1), blk_stride, tok_stride, k1, v1);
-      st.load(kbase, vbase, phys(2), blk_stride, tok_stride, k2, v2);
-      for (int i = 0; i < cnt; i += 4) {
-        st.load(kbase, vbase, phys(i + 3), blk_stride, tok_stride, k3, v3);
-        __builtin_amdgcn_sched_barrier(0);
-        visit(k0, v0, i);
-        st.load(kbase, vbase, phys(i + 4), blk_stride, tok_stride, k0, v0);
-        __builtin_amdgcn_sched_barrier(0);
-        visit(k1, v1, i + 1);
-        st.load(kbase, vbase, phys(i + 5), blk_stride, tok_stride, k1, v1);
-        __builtin_amdgcn_sched_barrier(0);
-        visit(k2, v2, i + 2);
-        st.load(kbase, vbase, phys(i + 6), blk_stride, tok_stride, k2, v2);
-        __builtin_amdgcn_sched_barrier(0);
-        visit(k3, v3, i + 3);
-      }
-    }
-  }
-  if (cur >= 0) finish(cur);
-}
-
-// Merge the pieces of every sequence that spans several workgroup ranges
-// (same flattened split as the persistent kernel); write zeros for a
-// sequence with no tokens.
-template <typename T, int D>
-__global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
-    const int32_t* __restrict__ ws_off, int num_seqs, int num_wgs, int num_heads,
-    const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
-    T* __restrict__ out, int64_t out_stride, PrefixArgs pfx, int block_size) {
-  const int sq = blockIdx.x;
-  const int hq = blockIdx.y;
-  const int d = threadIdx.x;
-  const int total = ws_off[num_seqs];
-  const int a = ws_off[sq], b = ws_off[sq + 1];
-  T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + d;
-  // blocks of this sequence attended by the shared-prefix pass, and its splits
-  const int skip = pfx.blocks ? ws_off[num_seqs + 1 + sq] : 0;
-  const int nsplit = (skip * block_size + kPrefixKeysPerSplit - 1) / kPrefixKeysPerSplit;
-  const int64_t pb = ((int64_t)sq * num_heads + hq) * kPrefixMaxSplits;
-  int g0 = 0, g1 = -1;    // ranges holding pieces of the walked blocks
-  if (a != b) {
-    const int per = (total + num_wgs - 1) / num_wgs;
-    g0 = a / per;
-    g1 = (b - 1) / per;
-    if (g0 == g1) return;   // finished (with its prefix) by the decode kernel
-  } else if (nsplit == 0) {
-    elem<T>::store(op, 0.0f);
-    return;
-  }
-  const int per = a != b ? (total + num_wgs - 1) / num_wgs : 1;
-  if (g1 - g0 <= 1 && nsplit <= 4) {
-    // At most two pieces and four prefix splits (the common case): every
-    // value is loaded in one round trip, then merged in the order of the
-    // general loop below (same operations, same results).
-    const int np = g1 - g0 + 1;
-    float pm[2], pl[2], pa[2], qm[4], ql[4], qa[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      pm[i] = kNegBig; pl[i] = 0.0f; pa[i] = 0.0f;
-      if (i < np) {
-        const int g = g0 + i;
-        const int slot = (a <= g * per) ? 0 : 1;
-        const int64_t base = ((int64_t)g * 2 + slot) * num_heads + hq;
-        pm[i] = ws_ml[base * 2];
-        pl[i] = ws_ml[base * 2 + 1];
-        pa[i] = ws_acc[base * D + d];
-      }
-    }
-#pragma unroll
-    for (int sp = 0; sp < 4; ++sp) {
-      qm[sp] = kNegBig; ql[sp] = 0.0f; qa[sp] = 0.0f;
-      if (sp < nsplit) {
-        qm[sp] = pfx.ml[(pb + sp) * 2];
-        ql[sp] = pfx.ml[(pb + sp) * 2 + 1];
-        qa[sp] = pfx.acc[(pb + sp) * D + d];
-      }
-    }
-    float M = kNegBig;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      if (i < np) M = fmaxf(M, pm[i]);
-#pragma unroll
-    for (int sp = 0; sp < 4; ++sp)
-      if (sp < nsplit) M = fmaxf(M, qm[sp]);
-    float L = 0.0f, O = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      if (i < np) {
-        const float f = pl[i] * fast_exp2(pm[i] - M);
-        L += f;
-        O = fmaf(pa[i], f, O);
-      }
-#pragma unroll
-    for (int sp = 0; sp < 4; ++sp)
-      if (sp < nsplit) {
-        const float f = ql[sp] * fast_exp2(qm[sp] - M);
-        L += f;
-        O = fmaf(qa[sp], f, O);
-      }
-    elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
-    return;
-  }
-  float M = kNegBig;
-  for (int g = g0; g <= g1; ++g) {
-    const int slot = (a <= g * per) ? 0 : 1;
-    M = fmaxf(M, ws_ml[(((int64_t)g * 2 + slot) * num_heads + hq) * 2]);
-  }
-  for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, pfx.ml[(pb + sp) * 2]);
-  float L = 0.0f, O = 0.0f;
-  for (int g = g0; g <= g1; ++g) {
-    const int slot = (a <= g * per) ? 0 : 1;
-    const int64_t base = ((int64_t)g * 2 + slot) * num_heads + hq;
-    const float f = ws_ml[base * 2 + 1] * fast_exp2(ws_ml[base * 2] - M);
-    L += f;
-    O = fmaf(ws_acc[base * D + d], f, O);
-  }
-  for (int sp = 0; sp < nsplit; ++sp) {
-    const float f = pfx.ml[(pb + sp) * 2 + 1] * fast_exp2(pfx.ml[(pb + sp) * 2] - M);
-    L += f;
-    O = fmaf(pfx.acc[(pb + sp) * D + d], f, O);
-  }
-  elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -757,19 +432,32 @@ __device__ __forceinline__ i16x4_t lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)p);
 }
 
-// PFX = false: prefill chunks (causal, normalised output rows).  PFX = true:
-// the shared-prefix pass -- workgroup (item, kv head) takes up to QT group
-// members against one 128-key split of the group's prefix (no causal mask;
-// every prefix key precedes every member's query) and writes prefix
-// partials.
+// Arguments of the MFMA attention body (prefill chunks or shared-prefix
+// units).
+template <typename T>
+struct ChunkArgs {
+  const T* __restrict__ q; int64_t q_stride;
+  const T* __restrict__ kc; const T* __restrict__ vc; int num_kv_heads; int64_t num_cache_blocks;
+  const int32_t* __restrict__ block_tables; int max_blocks;
+  const int32_t* __restrict__ cu; const int32_t* __restrict__ ctx; int seq_begin;
+  int nq_tiles, num_groups; float scale_log2; T* __restrict__ out; int64_t out_stride;
+  PrefixArgs pfx;
+};
+
+// PFX = false: prefill chunks (causal, normalised output rows); `unit` is
+// the workgroup id.  PFX = true: one shared-prefix unit -- `unit` is the
+// work item, `kvh_sel` the kv head: up to QT group members against one
+// 128-key split of the group's prefix (no causal mask; every prefix key
+// precedes every member's query), writing prefix partials.
+// The body runs on one team of W wavefronts (`tid` = thread index in the
+// team) with its own four LDS tiles.  Every early exit before the last
+// barrier depends only on (unit, its item), never on the team or the lane,
+// and teams that share a workgroup run the same item, so all wavefronts of
+// the workgroup meet the same barriers.
 template <typename T, int D, int G, int BS, int W, int BPW, bool PFX>
-__global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mfma_kernel(
-    const T* __restrict__ q, int64_t q_stride,
-    const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
-    const int32_t* __restrict__ block_tables, int max_blocks,
-    const int32_t* __restrict__ cu, const int32_t* __restrict__ ctx, int seq_begin,
-    int nq_tiles, int num_groups, float scale_log2, T* __restrict__ out, int64_t out_stride,
-    PrefixArgs pfx) {
+__device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit, int kvh_sel,
+                                                int tid, uint16_t* Ks0, uint16_t* Ks1,
+                                                uint16_t* Vs0, uint16_t* Vs1) {
   using M = Mfma32<T>;
   using v8 = typename M::v8;
   using L = ChunkLds<D, W * BPW>;
@@ -784,26 +472,34 @@ __global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mf
   constexpr int RPI = 64 / CPR;        // key rows per wave-wide 1 KiB load
   constexpr int LPW = BS / RPI;        // loads per wavefront per tile (one block each)
   static_assert(BS == 16 && (W == 4 || W == 8), "each wavefront stages one 16-token block");
-  // One LDS object per stage and operand: a load in flight into one stage
-  // provably does not alias the reads of the other, so the compiler does not
-  // make those reads wait for it.
-  __shared__ __align__(16) uint16_t Ks0[L::TILE], Ks1[L::TILE], Vs0[L::TILE], Vs1[L::TILE];
+  const T* __restrict__ q = A.q;
+  const int64_t q_stride = A.q_stride;
+  const T* __restrict__ kc = A.kc;
+  const T* __restrict__ vc = A.vc;
+  const int num_kv_heads = A.num_kv_heads;
+  const int64_t num_cache_blocks = A.num_cache_blocks;
+  const int max_blocks = A.max_blocks;
+  const float scale_log2 = A.scale_log2;
+  const PrefixArgs& pfx = A.pfx;
 
-  // XCD-aware order: workgroups are dispatched round-robin over the XCDs
-  // (id % kXcds), so workgroup id w serves (sequence, kv head) group
-  // (w / kXcds / nq) * kXcds + w % kXcds and query tile (w / kXcds) % nq:
-  // all query tiles of one group run on one XCD and share its L2 copy of
-  // the group's K/V, and consecutive groups alternate XCDs.
-  const int wg = (int)blockIdx.x;
+  // XCD-aware order (chunks): workgroups are dispatched round-robin over
+  // the XCDs (id % kXcds), so workgroup id w serves (sequence, kv head)
+  // group (w / kXcds / nq) * kXcds + w % kXcds and query tile
+  // (w / kXcds) % nq: all query tiles of one group run on one XCD and
+  // share its L2 copy of the group's K/V, and consecutive groups alternate
+  // XCDs.
   int kvh, seq, q0, qlen, qt0, pos0, kb0, kend, mbeg = 0, split = 0;
   if constexpr (PFX) {
-    const int item = wg / num_kv_heads;
-    kvh = wg % num_kv_heads;
+    const int item = unit;
+    kvh = kvh_sel;
     if (item >= pfx.max_items) return;
     const int4 it = *reinterpret_cast<const int4*>(pfx.items + 4 * item);
-    // unused item (leader < 0); rows beyond num_groups (= decode rows) and
-    // splits beyond the partial buffers are ignored
-    if (it.x < 0 || it.x >= num_groups || it.w < 0 || it.w >= kPrefixMaxSplits) return;
+    // unused item (leader < 0), leaders beyond the decode rows (num_groups),
+    // member slices outside `members` or wider than QT, splits beyond the
+    // partial buffers: skipped
+    if (it.x < 0 || it.x >= A.num_groups || it.w < 0 || it.w >= kPrefixMaxSplits || it.y < 0 ||
+        it.z < 1 || it.z > QT || it.y > pfx.num_members - it.z)
+      return;
     seq = it.x;                                 // the group leader's block table
     mbeg = it.y;
     qlen = it.z;                                // members in this item (<= QT)
@@ -814,30 +510,31 @@ __global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mf
     kb0 = split * kPrefixKeysPerSplit;
     kend = min(pkeys, kb0 + kPrefixKeysPerSplit);
     pos0 = 0x3fffffff;                          // queries follow every prefix key
-    if (kb0 >= kend || qlen <= 0) return;
+    if (kb0 >= kend) return;
   } else {
+    const int wg = unit;
     const int slot = wg / kXcds;
-    const int grp = (slot / nq_tiles) * kXcds + wg % kXcds;
-    if (grp >= num_groups) return;
+    const int grp = (slot / A.nq_tiles) * kXcds + wg % kXcds;
+    if (grp >= A.num_groups) return;
     kvh = grp % num_kv_heads;
-    seq = seq_begin + grp / num_kv_heads;
-    q0 = cu[seq];
-    qlen = cu[seq + 1] - q0;
-    qt0 = (slot % nq_tiles) * QT;
+    seq = A.seq_begin + grp / num_kv_heads;
+    q0 = A.cu[seq];
+    qlen = A.cu[seq + 1] - q0;
+    qt0 = (slot % A.nq_tiles) * QT;
     if (qt0 >= qlen) return;
-    const int ctxlen = min(ctx[seq], max_blocks * BS);
+    const int ctxlen = min(A.ctx[seq], max_blocks * BS);
     pos0 = ctxlen - qlen;                                      // position of chunk row 0
     kb0 = 0;
     kend = max(0, min(ctxlen, pos0 + min(qt0 + QT, qlen)));    // keys [0, kend)
     if (kend <= 0) return;
   }
   const int ntiles = (kend - kb0 + KT - 1) / KT;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int lr = lane & 31;        // this lane's query column / key row
   const int h = lane >> 5;         // half of the wavefront
   const int64_t tok_stride = (int64_t)num_kv_heads * D;
-  const int32_t* __restrict__ bt = block_tables + (int64_t)seq * max_blocks;
+  const int32_t* __restrict__ bt = A.block_tables + (int64_t)seq * max_blocks;
 
   // This lane's query row (the B-operand column of K Q^T).
   const int row = 32 * wave + lr;
@@ -847,7 +544,7 @@ __global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mf
   int qrow = PFX ? pfx.members[mbeg + min(qtok, qlen - 1)] : q0 + min(qtok, qlen - 1);
   bool qrow_ok = true;
   if constexpr (PFX) {
-    qrow_ok = qrow >= 0 && qrow < num_groups;
+    qrow_ok = qrow >= 0 && qrow < A.num_groups;
     qrow = qrow_ok ? qrow : seq;
   }
   v8 qf[QSTEPS];
@@ -890,7 +587,7 @@ __global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mf
   // Rows at or past kend hold data of the clamped block: zero their V so a
   // zero probability never meets a NaN (their scores are masked).
   auto zero_tail = [&](uint16_t* Vst, int k0) {
-    for (int c = threadIdx.x; c < KT * CPR; c += kThreads)
+    for (int c = tid; c < KT * CPR; c += kThreads)
       if (k0 + c / CPR >= kend) store16(Vst + (c / CPR) * D + 8 * (c % CPR), make_uint4(0, 0, 0, 0));
   };
 
@@ -1100,7 +797,7 @@ __global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mf
                         o[b][4 * g4 + 3] * inv);
     return;
   }
-  T* op = out + (int64_t)(q0 + qtok) * out_stride + (int64_t)(kvh * G + qg) * D + 4 * h;
+  T* op = A.out + (int64_t)(q0 + qtok) * A.out_stride + (int64_t)(kvh * G + qg) * D + 4 * h;
 #pragma unroll
   for (int b = 0; b < DBLK; ++b)
 #pragma unroll
@@ -1108,6 +805,363 @@ __global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mf
       *reinterpret_cast<uint2*>(op + 32 * b + 8 * g4) =
           make_uint2(M::pack2(o[b][4 * g4] * inv, o[b][4 * g4 + 1] * inv),
                      M::pack2(o[b][4 * g4 + 2] * inv, o[b][4 * g4 + 3] * inv));
+}
+
+
+// Prefill chunks (PFX = false) or the shared-prefix pass as a launch of its
+// own (PFX = true: workgroup = (item, kv head)).
+template <typename T, int D, int G, int BS, int W, int BPW, bool PFX>
+__global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mfma_kernel(
+    ChunkArgs<T> a) {
+  using L = ChunkLds<D, W * BPW>;
+  // One LDS object per stage and operand: a load in flight into one stage
+  // provably does not alias the reads of the other, so the compiler does not
+  // make those reads wait for it.
+  __shared__ __align__(16) uint16_t Ks0[L::TILE], Ks1[L::TILE], Vs0[L::TILE], Vs1[L::TILE];
+  const int wg = (int)blockIdx.x;
+  if constexpr (PFX)
+    chunk_mfma_body<T, D, G, BS, W, BPW, true>(a, wg / a.num_kv_heads, wg % a.num_kv_heads,
+                                               (int)threadIdx.x, Ks0, Ks1, Vs0, Vs1);
+  else
+    chunk_mfma_body<T, D, G, BS, W, BPW, false>(a, wg, 0, (int)threadIdx.x, Ks0, Ks1, Vs0, Vs1);
+}
+
+template <typename T, int D, int G, int BS, bool NT, int NBUF>
+__global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_kernel(
+    const T* __restrict__ q, int64_t q_stride,
+    const T* __restrict__ kc, const T* __restrict__ vc, int num_kv_heads, int64_t num_cache_blocks,
+    const int32_t* __restrict__ block_tables, int max_blocks, const int32_t* __restrict__ ctx,
+    int num_seqs, float scale_log2, T* __restrict__ out, int64_t out_stride,
+    int32_t* __restrict__ ws_off, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
+    PrefixArgs pfx) {
+  using S = HeadState<T, D, G, BS, NT>;
+  constexpr int VEC = S::VEC;
+  // LDS: s_off [num_seqs + 1], then (shared prefixes only) s_skip [num_seqs]
+  extern __shared__ int32_t s_off[];
+  int32_t* s_skip = s_off + num_seqs + 1;
+  __shared__ int32_t s_part[kPersistMaxWaves * 64];
+  const int max_tokens = max_blocks * BS;
+  const bool has_pfx = pfx.blocks != nullptr;
+  scan_block_counts<BS>(ctx, pfx.blocks, num_seqs, max_tokens, s_off, s_part, s_skip);
+  const int total = s_off[num_seqs];
+  const int H = num_kv_heads * G;
+  const int grid = (int)gridDim.x;
+
+  const RangeSplit rs = make_range_split(total, grid);
+  // ws_off: offsets [num_seqs + 1], then each sequence's skipped blocks
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i <= num_seqs; i += blockDim.x) {
+      ws_off[i] = s_off[i];
+      if (has_pfx && i < num_seqs) ws_off[num_seqs + 1 + i] = s_skip[i];
+    }
+  if (total == 0) return;
+  const int r0 = rs.start((int)blockIdx.x);
+  const int r1 = rs.start((int)blockIdx.x + 1);
+  if (r0 >= r1) return;
+
+  const int lane = threadIdx.x & 63;
+  const int kvh = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (kvh >= num_kv_heads) return;
+  const int64_t tok_stride = (int64_t)num_kv_heads * D;
+  const int64_t blk_stride = (int64_t)BS * tok_stride;
+
+  S st;
+  st.tg = lane / S::RL;
+  st.dc = lane % S::RL;
+  const int64_t lane_off = (int64_t)kvh * D + st.dc * VEC + st.tg * tok_stride;
+  const T* kbase = kc + lane_off;
+  const T* vbase = vc + lane_off;
+
+  int cur = -1;     // sequence whose state st holds (uniform)
+  int cur_end = 0;  // its context length
+  int cur_skip = 0; // its leading blocks attended by the shared-prefix units
+
+  // Finish sequence sq: a piece covering the whole sequence goes straight
+  // to `out` (merged with the row's shared-prefix partials, which the
+  // prefix launch before this one wrote), any other piece to this
+  // workgroup's slot 0 (first piece) or 1 (last), for the reduce kernel.
+  auto finish = [&](int sq) __attribute__((always_inline)) {
+    st.merge_token_groups();
+    const int a = s_off[sq], b = s_off[sq + 1];
+    const bool whole = a >= r0 && b <= r1;
+    if (st.tg != 0) return;
+    {
+      if (whole && cur_skip > 0) {
+        // fold in the prefix partials (splits of 128 keys), then normalise
+        const int nsplit = (cur_skip * BS + kPrefixKeysPerSplit - 1) / kPrefixKeysPerSplit;
+        if constexpr (G <= 2) {
+          if (nsplit <= 4) {
+            // up to four splits: every partial is loaded in one round trip,
+            // then merged in the order of the general loop below
+            float qm[G][4], ql[G][4], qa[G][4][S::VEC];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const int64_t pb = ((int64_t)sq * H + kvh * G + g) * kPrefixMaxSplits;
+#pragma unroll
+              for (int sp = 0; sp < 4; ++sp) {
+                qm[g][sp] = kNegBig;
+                ql[g][sp] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < S::VEC; ++j) qa[g][sp][j] = 0.0f;
+                if (sp < nsplit) {
+                  qm[g][sp] = pfx.ml[(pb + sp) * 2];
+                  ql[g][sp] = pfx.ml[(pb + sp) * 2 + 1];
+                  const float* ap = pfx.acc + (pb + sp) * D + st.dc * VEC;
+#pragma unroll
+                  for (int j = 0; j < S::VEC; ++j) qa[g][sp][j] = ap[j];
+                }
+              }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const int hq = kvh * G + g;
+              float mx = st.m[g];
+#pragma unroll
+              for (int sp = 0; sp < 4; ++sp)
+                if (sp < nsplit) mx = fmaxf(mx, qm[g][sp]);
+              const float fs = fast_exp2(st.m[g] - mx);
+              float L = st.l[g] * fs;
+              float o[S::VEC];
+#pragma unroll
+              for (int j = 0; j < S::VEC; ++j) o[j] = st.acc[g][j] * fs;
+#pragma unroll
+              for (int sp = 0; sp < 4; ++sp)
+                if (sp < nsplit) {
+                  const float f = ql[g][sp] * fast_exp2(qm[g][sp] - mx);
+                  L += f;
+#pragma unroll
+                  for (int j = 0; j < S::VEC; ++j) o[j] = fmaf(qa[g][sp][j], f, o[j]);
+                }
+              const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+              T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + st.dc * VEC;
+#pragma unroll
+              for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, o[j] * inv);
+            }
+            return;
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const int hq = kvh * G + g;
+          const int64_t pb = ((int64_t)sq * H + hq) * kPrefixMaxSplits;
+          float mx = st.m[g];
+          for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, pfx.ml[(pb + sp) * 2]);
+          const float fs = fast_exp2(st.m[g] - mx);
+          float L = st.l[g] * fs;
+          float o[S::VEC];
+#pragma unroll
+          for (int j = 0; j < S::VEC; ++j) o[j] = st.acc[g][j] * fs;
+          for (int sp = 0; sp < nsplit; ++sp) {
+            const float f = pfx.ml[(pb + sp) * 2 + 1] * fast_exp2(pfx.ml[(pb + sp) * 2] - mx);
+            L += f;
+            const float* ap = pfx.acc + (pb + sp) * D + st.dc * VEC;
+#pragma unroll
+            for (int j = 0; j < S::VEC; ++j) o[j] = fmaf(ap[j], f, o[j]);
+          }
+          const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+          T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + st.dc * VEC;
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, o[j] * inv);
+        }
+        return;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int hq = kvh * G + g;
+      const float inv = st.l[g] > 0.0f ? 1.0f / st.l[g] : 0.0f;
+      if (whole) {
+        T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + st.dc * VEC;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, st.acc[g][j] * inv);
+      } else {
+        const int slot = (a <= r0) ? 0 : 1;
+        const int64_t base = ((int64_t)blockIdx.x * 2 + slot) * H + hq;
+        float* wp = ws_acc + base * D + st.dc * VEC;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) wp[j] = st.acc[g][j] * inv;
+        if (st.dc == 0) { ws_ml[base * 2] = st.m[g]; ws_ml[base * 2 + 1] = st.l[g]; }
+      }
+    }
+  };
+
+  static_assert(NBUF == 2 || NBUF == 4, "NBUF");
+  uint4 k0[S::LOADS], v0[S::LOADS], k1[S::LOADS], v1[S::LOADS];
+  uint4 k2[NBUF == 4 ? S::LOADS : 1], v2[NBUF == 4 ? S::LOADS : 1];
+  uint4 k3[NBUF == 4 ? S::LOADS : 1], v3[NBUF == 4 ? S::LOADS : 1];
+  for (int base = r0; base < r1; base += 64) {
+    const int cnt = min(64, r1 - base);
+    // Lane i resolves flattened entry base + i: its sequence, logical block
+    // and physical block id.
+    int lseq = 0, lblk = 0, id = 0;
+    if (lane < cnt) {
+      const int j = base + lane;
+      int lo = 0, hi = num_seqs - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_off[mid] <= j) lo = mid; else hi = mid - 1;
+      }
+      lseq = lo;
+      lblk = j - s_off[lo] + (has_pfx ? s_skip[lo] : 0);   // block index in the table
+      id = block_tables[(int64_t)lo * max_blocks + lblk];
+    }
+    if (id < 0 || id >= num_cache_blocks) id = 0;
+    auto phys = [&](int i) { return __builtin_amdgcn_readlane(id, min(i, cnt - 1)); };
+    // Start (or continue) the sequence of entry i, then fold its block in;
+    // i >= cnt is a fully masked no-op so process() always runs.
+    auto visit = [&](const uint4* kk, const uint4* vv, int i) {
+      const bool real = i < cnt;
+      const int sq = __builtin_amdgcn_readlane(lseq, min(i, cnt - 1));
+      const int lb = __builtin_amdgcn_readlane(lblk, min(i, cnt - 1));
+      if (real && sq != cur) {
+        if (cur >= 0) finish(cur);
+        cur = sq;
+        cur_end = min(max(ctx[sq], 0), max_tokens);
+        cur_skip = has_pfx ? s_skip[sq] : 0;
+        st.init(q + (int64_t)sq * q_stride + (int64_t)kvh * G * D, scale_log2, lane);
+      }
+      st.process(kk, vv, lb, real ? cur_end : -1);
+    };
+    // NBUF register buffers rotate: NBUF - 1 blocks are in flight while one
+    // is folded in.  Loads past the group end reload its last block (cache
+    // hit) and their visits are masked no-ops.
+    if constexpr (NBUF == 2) {
+      st.load(kbase, vbase, phys(0), blk_stride, tok_stride, k0, v0);
+      for (int i = 0; i < cnt; i += 2) {
+        st.load(kbase, vbase, phys(i + 1), blk_stride, tok_stride, k1, v1);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k0, v0, i);
+        st.load(kbase, vbase, phys(i + 2), blk_stride, tok_stride, k0, v0);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k1, v1, i + 1);
+      }
+    } else {
+      st.load(kbase, vbase, phys(0), blk_stride, tok_stride, k0, v0);
+      st.load(kbase, vbase, phys(1), blk_stride, tok_stride, k1, v1);
+      st.load(kbase, vbase, phys(2), blk_stride, tok_stride, k2, v2);
+      for (int i = 0; i < cnt; i += 4) {
+        st.load(kbase, vbase, phys(i + 3), blk_stride, tok_stride, k3, v3);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k0, v0, i);
+        st.load(kbase, vbase, phys(i + 4), blk_stride, tok_stride, k0, v0);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k1, v1, i + 1);
+        st.load(kbase, vbase, phys(i + 5), blk_stride, tok_stride, k1, v1);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k2, v2, i + 2);
+        st.load(kbase, vbase, phys(i + 6), blk_stride, tok_stride, k2, v2);
+        __builtin_amdgcn_sched_barrier(0);
+        visit(k3, v3, i + 3);
+      }
+    }
+  }
+  if (cur >= 0) finish(cur);
+}
+
+// Merge the pieces of every sequence that spans several workgroup ranges
+// (same flattened split as the persistent kernel), together with its
+// shared-prefix partials if it has any; write zeros for a sequence with no
+// tokens.  Partials are merged in a fixed order: walked pieces in range
+// order, then prefix splits in key order.
+template <typename T, int D>
+__global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
+    const int32_t* __restrict__ ws_off, int num_seqs, int num_wgs, int num_heads,
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
+    T* __restrict__ out, int64_t out_stride, PrefixArgs pfx, int block_size) {
+  const int sq = blockIdx.x;
+  const int hq = blockIdx.y;
+  const int d = threadIdx.x;
+  const int a = ws_off[sq], b = ws_off[sq + 1];
+  const RangeSplit rs = make_range_split(ws_off[num_seqs], num_wgs);
+  T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + d;
+  // blocks of this sequence attended by the shared-prefix pass, and its splits
+  const int skip = pfx.blocks ? ws_off[num_seqs + 1 + sq] : 0;
+  const int nsplit = (skip * block_size + kPrefixKeysPerSplit - 1) / kPrefixKeysPerSplit;
+  const int64_t pb = ((int64_t)sq * num_heads + hq) * kPrefixMaxSplits;
+  int g0 = 0, np = 0;          // walked pieces: ranges g0 .. g0 + np - 1
+  if (a != b) {
+    g0 = rs.owner(a);
+    const int g1 = rs.owner(b - 1);
+    if (g0 == g1) return;      // finished (with its prefix) by the decode kernel
+    np = g1 - g0 + 1;
+  } else if (nsplit == 0) {
+    elem<T>::store(op, 0.0f);
+    return;
+  }
+  // (m, l, acc[d]) of walked piece i
+  auto piece = [&](int i, float& m, float& l, float& v) {
+    const int g = g0 + i;
+    const int slot = (a <= rs.start(g)) ? 0 : 1;
+    const int64_t base = ((int64_t)g * 2 + slot) * num_heads + hq;
+    m = ws_ml[base * 2];
+    l = ws_ml[base * 2 + 1];
+    v = ws_acc[base * D + d];
+  };
+  if (np <= 2 && nsplit <= 4) {
+    // At most two pieces and four prefix splits (the common case): every
+    // value is loaded in one round trip, then merged in the order of the
+    // general loop below (same operations, same results).
+    float pm[2], pl[2], pa[2], qm[4], ql[4], qa[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      pm[i] = kNegBig; pl[i] = 0.0f; pa[i] = 0.0f;
+      if (i < np) piece(i, pm[i], pl[i], pa[i]);
+    }
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp) {
+      qm[sp] = kNegBig; ql[sp] = 0.0f; qa[sp] = 0.0f;
+      if (sp < nsplit) {
+        qm[sp] = pfx.ml[(pb + sp) * 2];
+        ql[sp] = pfx.ml[(pb + sp) * 2 + 1];
+        qa[sp] = pfx.acc[(pb + sp) * D + d];
+      }
+    }
+    float M = kNegBig;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (i < np) M = fmaxf(M, pm[i]);
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp)
+      if (sp < nsplit) M = fmaxf(M, qm[sp]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (i < np) {
+        const float f = pl[i] * fast_exp2(pm[i] - M);
+        L += f;
+        O = fmaf(pa[i], f, O);
+      }
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp)
+      if (sp < nsplit) {
+        const float f = ql[sp] * fast_exp2(qm[sp] - M);
+        L += f;
+        O = fmaf(qa[sp], f, O);
+      }
+    elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
+    return;
+  }
+  float M = kNegBig;
+  for (int i = 0; i < np; ++i) {
+    float m, l, v;
+    piece(i, m, l, v);
+    M = fmaxf(M, m);
+  }
+  for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, pfx.ml[(pb + sp) * 2]);
+  float L = 0.0f, O = 0.0f;
+  for (int i = 0; i < np; ++i) {
+    float m, l, v;
+    piece(i, m, l, v);
+    const float f = l * fast_exp2(m - M);
+    L += f;
+    O = fmaf(v, f, O);
+  }
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float f = pfx.ml[(pb + sp) * 2 + 1] * fast_exp2(pfx.ml[(pb + sp) * 2] - M);
+    L += f;
+    O = fmaf(pfx.acc[(pb + sp) * D + d], f, O);
+  }
+  elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
 }
 
 // Merge the partitions of one (row, query head); rows with a single
@@ -1248,11 +1302,11 @@ static void launch_persistent(const void* q, int64_t q_stride, const void* kc, c
   if constexpr (!std::is_same<T, float>::value && (D == 64 || D == 128) && BS == 16) {
     if (pfx.blocks && pfx.max_items > 0) {
       // shared prefixes first: their partials are read by the two kernels below
+      const ChunkArgs<T> ca{(const T*)q, q_stride, (const T*)kc, (const T*)vc, num_kv_heads,
+                            num_cache_blocks, bt, max_blocks, nullptr, ctx, 0, 1, num_seqs,
+                            scale_log2, (T*)out, out_stride, pfx};
       hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16, 4, 1, true>),
-                         dim3((unsigned)(pfx.max_items * num_kv_heads)), dim3(256), 0, st,
-                         (const T*)q, q_stride, (const T*)kc, (const T*)vc, num_kv_heads,
-                         num_cache_blocks, bt, max_blocks, nullptr, ctx, 0, 1, num_seqs, scale_log2,
-                         (T*)out, out_stride, pfx);
+                         dim3((unsigned)(pfx.max_items * num_kv_heads)), dim3(256), 0, st, ca);
     }
   }
   const size_t lds = sizeof(int32_t) * (size_t)(num_seqs + 1 + (pfx.blocks ? num_seqs : 0));
@@ -1343,11 +1397,12 @@ static void launch_chunk_kernel_w(const LaunchArgs& a, const int32_t* cu, int se
   const int nq = (max_query_len + QT - 1) / QT;
   const int groups = a.num_kv_heads * n_seqs;
   const int64_t wgs = (int64_t)((groups + kXcds - 1) / kXcds) * kXcds * nq;
+  const ChunkArgs<T> ca{(const T*)a.q, a.q_stride, (const T*)a.kc, (const T*)a.vc,
+                        a.num_kv_heads, a.num_cache_blocks, a.bt, a.max_blocks, cu, a.ctx,
+                        seq_begin, nq, groups, a.scale_log2, (T*)a.out, a.out_stride,
+                        PrefixArgs{}};
   hipLaunchKernelGGL((attn_chunk_mfma_kernel<T, D, G, 16, W, BPW, false>), dim3((unsigned)wgs),
-                     dim3(64 * W), 0, a.st, (const T*)a.q, a.q_stride, (const T*)a.kc,
-                     (const T*)a.vc, a.num_kv_heads, a.num_cache_blocks, a.bt, a.max_blocks, cu,
-                     a.ctx, seq_begin, nq, groups, a.scale_log2, (T*)a.out, a.out_stride,
-                     PrefixArgs{});
+                     dim3(64 * W), 0, a.st, ca);
 }
 
 // Chunk workgroup shape (LV_ATTN_CHUNK_CFG): 1 = 4 wavefronts x 64-key tiles
@@ -1448,6 +1503,8 @@ static int paged_attention_impl(const void* query_dev, int64_t q_stride_t,
              "lv_paged_attention: token strides smaller than num_heads*head_dim");
   LV_REQUIRE((int64_t)max_blocks * block_size <= (1ll << 24),
              "lv_paged_attention: max_blocks * block_size above 2^24 tokens");
+  LV_REQUIRE((int64_t)num_decodes * max_blocks <= (1ll << 31) - (1ll << 16),
+             "lv_paged_attention: num_decodes * max_blocks above 2^31 - 2^16");
 
   const int G = num_heads / num_kv_heads;
   const float scale_log2 = scale * 0x1.715476p+0f;
@@ -1543,13 +1600,13 @@ extern "C" int lv_paged_attention_prefix(
     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
     void* out_dev, int64_t out_stride_t, void* workspace_dev, size_t workspace_bytes,
     const int32_t* prefix_blocks_dev, const int32_t* prefix_items_dev, int32_t max_items,
-    const int32_t* prefix_members_dev, void* prefix_workspace_dev, size_t prefix_workspace_bytes,
-    lv_dtype dtype, void* stream) {
+    const int32_t* prefix_members_dev, int32_t num_members, void* prefix_workspace_dev,
+    size_t prefix_workspace_bytes, lv_dtype dtype, void* stream) {
   using namespace lv;
   clear_error();
   LV_REQUIRE(num_decodes >= 1 && num_decodes <= kPrefixMaxRows,
              "lv_paged_attention_prefix: num_decodes must be in [1, %d]", kPrefixMaxRows);
-  LV_REQUIRE(prefix_blocks_dev && prefix_members_dev && max_items >= 0 &&
+  LV_REQUIRE(prefix_blocks_dev && prefix_members_dev && max_items >= 0 && num_members >= 0 &&
                  (prefix_items_dev || max_items == 0),
              "lv_paged_attention_prefix: null prefix description");
   LV_REQUIRE((reinterpret_cast<uintptr_t>(prefix_items_dev) & 15) == 0,
@@ -1567,6 +1624,7 @@ extern "C" int lv_paged_attention_prefix(
   pa.items = prefix_items_dev;
   pa.members = prefix_members_dev;
   pa.max_items = max_items;
+  pa.num_members = num_members;
   pa.ml = (float*)prefix_workspace_dev;
   pa.acc = (float*)((char*)prefix_workspace_dev + align256(n * 2 * sizeof(float)));
   return paged_attention_impl(query_dev, q_stride_t, key_cache_dev, value_cache_dev,

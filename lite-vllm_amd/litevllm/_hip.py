@@ -18,7 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 LV_F32, LV_F16, LV_BF16 = 0, 1, 2
 LV_ACT_NONE, LV_ACT_SILU_MUL = 0, 1
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Every symbol the header declares, with (restype, argtypes).
 _c_i32, _c_i64, _c_f32, _c_p, _c_sz = (
@@ -73,7 +73,8 @@ SIGNATURES: dict[str, tuple] = {
         _c_p, _c_i64,                 # out, out_stride_t
         _c_p, _c_sz,                  # workspace, workspace_bytes
         _c_p, _c_p, _c_i32,           # prefix_blocks, prefix_items, max_items
-        _c_p, _c_p, _c_sz,            # prefix_members, prefix_workspace, its bytes
+        _c_p, _c_i32,                 # prefix_members, num_members
+        _c_p, _c_sz,                  # prefix_workspace, its bytes
         ctypes.c_int, _c_p,           # dtype, stream
     ]),
     "lv_sample_workspace_size": (ctypes.c_size_t, [_c_i64, _c_i64]),

@@ -123,6 +123,7 @@ def _workspace(device: torch.device, nbytes: int, kind: str = "attn") -> Optiona
 PREFIX_KEYS_PER_SPLIT = 128
 PREFIX_MAX_BLOCKS = 128
 PREFIX_ROWS_PER_ITEM = 128
+PREFIX_MAX_SPLITS = 16
 PREFIX_MAX_DECODES = 7000
 
 
@@ -182,7 +183,46 @@ def prefix_plan_arrays(groups, num_decodes: int, group_size: int, block_size: in
         members = np.concatenate([members, np.zeros(max_members - members.size, np.int32)])
     items_a = np.asarray(items, np.int32).reshape(-1, 4)
     members_a = members.astype(np.int32) if members.size else np.zeros(1, np.int32)
+    check_prefix_plan(blocks, items_a, members_a, group_size, block_size)
     return blocks, items_a, members_a
+
+
+def check_prefix_plan(blocks, items, members, group_size: int, block_size: int = 16) -> None:
+    """Raise ValueError unless host arrays (numpy) form a plan that
+    lv_paged_attention_prefix computes correctly: every used item's (leader
+    >= 0) leader, split and member slice in range; every member of a
+    slice shares the leader's prefix length; and every row with a prefix
+    covered by exactly one item for each 128-key split of it.  (The kernels
+    skip out-of-range items, but a row left uncovered would merge a stale
+    partial.)"""
+    import numpy as np
+    blocks = np.asarray(blocks, np.int64)
+    items = np.asarray(items, np.int64).reshape(-1, 4)
+    members = np.asarray(members, np.int64).reshape(-1)
+    n = blocks.shape[0]
+    it = items[items[:, 0] >= 0]
+    leader, first, cnt, split = it[:, 0], it[:, 1], it[:, 2], it[:, 3]
+    per_item = PREFIX_ROWS_PER_ITEM // group_size
+    if ((leader >= n) | (split < 0) | (split >= PREFIX_MAX_SPLITS)
+            | (cnt < 1) | (cnt > per_item) | (first < 0) | (first + cnt > members.size)).any():
+        raise ValueError("prefix plan: an item's leader, split or member slice is out of range")
+    if ((blocks < 0) | (blocks > PREFIX_MAX_BLOCKS)).any():
+        raise ValueError(f"prefix plan: prefix lengths must lie in [0, {PREFIX_MAX_BLOCKS}]")
+    nsplit = -(-blocks * block_size // PREFIX_KEYS_PER_SPLIT)
+    if (blocks[leader] <= 0).any() or (split >= nsplit[leader]).any():
+        raise ValueError("prefix plan: an item's split lies past its leader's prefix")
+    def ranks(counts):   # 0..c-1 for each count c, concatenated
+        return np.arange(int(counts.sum())) - np.repeat(np.cumsum(counts) - counts, counts)
+    rows = members[np.repeat(first, cnt) + ranks(cnt)]
+    splits = np.repeat(split, cnt)
+    leads = np.repeat(leader, cnt)
+    if ((rows < 0) | (rows >= n)).any() or (blocks[rows] != blocks[leads]).any():
+        raise ValueError("prefix plan: a member row is out of range or has another prefix length")
+    covered = rows * 32 + splits
+    need = np.repeat(np.arange(n), nsplit) * 32 + ranks(nsplit)
+    if covered.size != need.size or not np.array_equal(np.sort(covered), np.sort(need)):
+        raise ValueError("prefix plan: every (row, split) of a prefix must be covered by "
+                         "exactly one item")
 
 
 def prefix_attention_supported(num_heads: int, num_kv_heads: int, head_dim: int,
@@ -322,7 +362,7 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
         B, num_decodes, T, max_query_len, H, hkv, D, bs, float(scale),
         _ptr(out), out.stride(0), _ptr(ws), 0 if ws is None else ws.numel(),
         _ptr(prefix.blocks), _ptr(prefix.items), prefix.items.shape[0], _ptr(prefix.members),
-        _ptr(pws), 0 if pws is None else pws.numel(), dt, _stream(dev))
+        prefix.members.shape[0], _ptr(pws), 0 if pws is None else pws.numel(), dt, _stream(dev))
     _hip.check(rc, "lv_paged_attention_prefix")
     return out
 

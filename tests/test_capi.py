@@ -67,11 +67,11 @@ def test_prefix_entry_host_side_checks():
     fake16, fake4 = 0x1000, 0x1004
 
     def call(num_decodes=8, blocks=fake16, items=fake16, max_items=4, members=fake16,
-             pws=fake16, pws_bytes=1 << 30):
+             num_members=8, pws=fake16, pws_bytes=1 << 30):
         return lib.lv_paged_attention_prefix(
             None, 0, None, None, 1, None, 1, None, None, num_decodes, num_decodes,
             num_decodes, 1, 16, 8, 128, 16, 0.1, None, 0, None, 0,
-            blocks, items, max_items, members, pws, pws_bytes, _hip.LV_BF16, None)
+            blocks, items, max_items, members, num_members, pws, pws_bytes, _hip.LV_BF16, None)
 
     assert call(num_decodes=0) == -1 and b"num_decodes" in lib.lv_last_error()
     assert call(num_decodes=7001) == -1 and b"num_decodes" in lib.lv_last_error()
@@ -79,6 +79,7 @@ def test_prefix_entry_host_side_checks():
     assert call(members=None) == -1 and b"null prefix" in lib.lv_last_error()
     assert call(items=None) == -1 and b"null prefix" in lib.lv_last_error()
     assert call(max_items=-1) == -1 and b"null prefix" in lib.lv_last_error()
+    assert call(num_members=-1) == -1 and b"null prefix" in lib.lv_last_error()
     assert call(items=fake4) == -1 and b"16-byte aligned" in lib.lv_last_error()
     need = lib.lv_paged_attention_prefix_workspace_size(8, 16, 128)
     assert call(pws_bytes=need - 1) == -3 and b"prefix workspace" in lib.lv_last_error()

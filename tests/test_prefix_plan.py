@@ -129,3 +129,27 @@ def test_find_shared_prefixes_caps_at_the_context():
     descs, flat = _step(tables, ctx)
     got = find_shared_prefixes(descs, flat, 3, 16, 2, min_saved=0)
     assert [(list(map(int, r)), n) for r, n in got] == [([0, 1, 2], 9)]
+
+
+def test_check_prefix_plan_rejects_inconsistent_plans():
+    """check_prefix_plan accepts what prefix_plan_arrays builds and refuses
+    each way a hand-made plan could leave a prefix row with a stale or
+    doubled partial."""
+    blocks, items, members = ops.prefix_plan_arrays(
+        [([3, 4, 5], 9), (list(range(10, 80)), 16)], num_decodes=100, group_size=2,
+        max_items=8)
+    ops.check_prefix_plan(blocks, items, members, 2)
+
+    def bad(mutate, match):
+        b, it, m = blocks.copy(), items.copy(), members.copy()
+        mutate(b, it, m)
+        with pytest.raises(ValueError, match=match):
+            ops.check_prefix_plan(b, it, m, 2)
+
+    bad(lambda b, it, m: it.__setitem__((0, 0), -1), "exactly one item")   # item dropped
+    bad(lambda b, it, m: it.__setitem__((1, 2), 65), "out of range")       # slice wider than 64
+    bad(lambda b, it, m: it.__setitem__((1, 1), 200), "out of range")      # slice past members
+    bad(lambda b, it, m: it.__setitem__((1, 3), 3), "past its leader")     # split past the prefix
+    bad(lambda b, it, m: b.__setitem__(4, 8), "another prefix length")     # member disagrees
+    bad(lambda b, it, m: b.__setitem__(50 + 30, 16), "exactly one item")   # row 80 uncovered
+    bad(lambda b, it, m: it.__setitem__(6, it[5]), "exactly one item")     # doubled item
