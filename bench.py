@@ -258,7 +258,7 @@ def bench_e2e(args):
     time.  The decode-attention launches of decode-only steps are bracketed
     by HIP events on the launch stream for the roofline."""
     import torch
-    from litevllm import LLM, SamplingParams, ops, workloads
+    from litevllm import LLM, SamplingParams, _hip, workloads
     from litevllm.engine import model_runner as mr
 
     mc = workloads.QWEN3_06B_SHAPE
@@ -267,15 +267,18 @@ def bench_e2e(args):
     hkv, D, H = mc["num_key_value_heads"], mc["head_dim"], mc["num_attention_heads"]
 
     # -- instrumentation of decode attention in decode-only steps: HIP events
-    # on the launch stream around each lv_paged_attention call of an eager
-    # step.  A captured graph cannot hold timing events on ROCm, so with
-    # graphs on, one decode step in SAMPLE_EVERY runs eagerly (same kernel,
+    # on the launch stream right around the C-ABI call (lv_paged_attention /
+    # lv_paged_attention_prefix, which enqueues the call's kernels) of an
+    # eager step, so the interval is the kernels' GPU time, not the Python
+    # wrapper's.  A captured graph cannot hold timing events on ROCm, so with
+    # graphs on, one decode step in SAMPLE_EVERY runs eagerly (same kernels,
     # same data) and is the timing sample; the others replay graphs.
     SAMPLE_EVERY = 32
     probe = {"on": False, "meta": None, "durs": [], "bytes": 0, "decode_steps": 0}
     orig_exec = mr.ModelRunner.execute_model
-    orig_attn = ops.paged_attention
     orig_accepts = mr.DecodeGraphs.accepts
+    lib = _hip.load()
+    orig_c = {n: getattr(lib, n) for n in ("lv_paged_attention", "lv_paged_attention_prefix")}
 
     def step_bytes(meta):
         """K/V rows each read once per row -- a block that the step's
@@ -292,18 +295,22 @@ def bench_e2e(args):
         probe["meta"] = meta
         return orig_exec(self, meta)
 
-    def attn_probe(query, *a, **kw):
-        meta = probe["meta"]
-        if not probe["on"] or meta is None or meta.num_decodes != len(meta.seq_ids):
-            return orig_attn(query, *a, **kw)
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        out = orig_attn(query, *a, **kw)
-        e1.record()
-        probe["durs"].append((e0, e1))
-        probe["bytes"] += step_bytes(meta)
-        return out
+    def c_probe(name):
+        fn = orig_c[name]
+
+        def call(*args):
+            meta = probe["meta"]
+            if not probe["on"] or meta is None or meta.num_decodes != len(meta.seq_ids):
+                return fn(*args)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            rc = fn(*args)
+            e1.record()
+            probe["durs"].append((e0, e1))
+            probe["bytes"] += step_bytes(meta)
+            return rc
+        return call
 
     def accepts_probe(self, st):
         ok = orig_accepts(self, st)
@@ -314,7 +321,8 @@ def bench_e2e(args):
         return ok
 
     mr.ModelRunner.execute_model = exec_probe
-    ops.paged_attention = attn_probe
+    for n in orig_c:
+        setattr(lib, n, c_probe(n))
     mr.DecodeGraphs.accepts = accepts_probe
     llm = LLM("qwen3-0.6b-shape", dtype="bfloat16", load_format="dummy", hf_overrides=mc,
               skip_tokenizer_init=True, enable_prefix_caching=True, max_num_batched_tokens=8192,
@@ -349,7 +357,8 @@ def bench_e2e(args):
     wall = time.perf_counter() - t0
     probe["on"] = False
     mr.ModelRunner.execute_model = orig_exec
-    ops.paged_attention = orig_attn
+    for n, fn in orig_c.items():
+        setattr(lib, n, fn)
     mr.DecodeGraphs.accepts = orig_accepts
     durs = [a.elapsed_time(b) for a, b in probe["durs"]]
     cpu_state = cpu_cfg = None

@@ -1,89 +1,188 @@
-"""AsyncLLM — streaming generation (reference entrypoints/async_llm.py:
-25-126): engine steps run on an executor thread, one asyncio.Queue per
-request, text deltas streamed, a None sentinel ends a stream."""
+"""AsyncLLM: streaming generation on top of LLMEngine.
+
+Public API of the reference's AsyncLLM (entrypoints/async_llm.py:25-126):
+``initialize``, ``add_request``, ``stream`` (text deltas), ``generate``,
+``abort``, ``has_unfinished``.
+
+Design: one engine thread owns the LLMEngine for its whole life.  The
+asyncio side never touches engine state; it posts commands (add, abort,
+stop) to the thread's inbox, and the thread applies them between two
+``LLMEngine.step`` calls, so the scheduler and the block manager only ever
+change on that thread (an abort can never land between a step's schedule
+and its packing).  The thread hands each step's outputs back to the event
+loop with ``call_soon_threadsafe``; every request has its own
+``asyncio.Queue`` of deltas closed by an end marker.  If a step raises,
+the error is delivered to every open stream (each ``stream`` raises it)
+and later requests are refused.  A consumer that stops reading a stream
+early aborts its request, which frees its KV blocks.
+"""
 
 from __future__ import annotations
 
 import asyncio
+import threading
 import uuid
+from collections import deque
 from typing import AsyncIterator, Optional
 
 from litevllm.config import EngineConfig, SamplingParams
 from litevllm.engine.llm_engine import LLMEngine
+
+_END = object()          # end of a stream
+
+
+class _Failed:
+    """A stream item carrying the engine thread's exception."""
+
+    def __init__(self, exc: BaseException) -> None:
+        self.exc = exc
 
 
 class AsyncLLM:
     def __init__(self, engine_config: EngineConfig) -> None:
         self.config = engine_config
         self._engine: Optional[LLMEngine] = None
-        self._request_streams: dict[str, asyncio.Queue] = {}
-        self._step_task: Optional[asyncio.Task] = None
-        self._running = False
+        self._loop: Optional[asyncio.AbstractEventLoop] = None
+        self._streams: dict[str, asyncio.Queue] = {}
+        self._inbox: deque = deque()               # (command, payload), loop -> engine thread
+        self._wake = threading.Condition()
+        self._thread: Optional[threading.Thread] = None
+        self._error: Optional[BaseException] = None
 
+    # -- lifecycle ---------------------------------------------------------
     async def initialize(self) -> None:
-        self._engine = LLMEngine(self.config)
-        self._engine.stream_text = True
-        await asyncio.get_running_loop().run_in_executor(None, self._engine.initialize)
+        """Load the model and start the engine thread."""
+        self._loop = asyncio.get_running_loop()
+        engine = LLMEngine(self.config)
+        engine.stream_text = True
+        await self._loop.run_in_executor(None, engine.initialize)
+        self._engine = engine
+        self._thread = threading.Thread(target=self._run_engine, name="litevllm-engine",
+                                        daemon=True)
+        self._thread.start()
 
+    async def shutdown(self) -> None:
+        """Stop the engine thread (unfinished requests are dropped)."""
+        if self._thread is not None:
+            self._post("stop", None)
+            await self._loop.run_in_executor(None, self._thread.join)
+            self._thread = None
+
+    # -- requests ------------------------------------------------------------
     async def add_request(self, prompt: Optional[str], sampling_params: SamplingParams,
                           request_id: Optional[str] = None,
                           prompt_token_ids: Optional[list[int]] = None) -> str:
+        if self._thread is None:
+            raise RuntimeError("AsyncLLM is not initialized (await initialize() first)")
+        if self._error is not None:
+            raise RuntimeError("the engine thread failed") from self._error
         if request_id is None:
             request_id = str(uuid.uuid4())
-        self._request_streams[request_id] = asyncio.Queue()
-        self._engine.add_request(prompt, sampling_params, request_id, prompt_token_ids)
-        self._ensure_step_loop()
+        if request_id in self._streams:
+            raise ValueError(f"request {request_id!r} is already running")
+        self._streams[request_id] = asyncio.Queue()
+        self._post("add", (request_id, prompt, sampling_params, prompt_token_ids))
         return request_id
 
     async def stream(self, prompt: Optional[str], sampling_params: Optional[SamplingParams] = None,
                      request_id: Optional[str] = None,
                      prompt_token_ids: Optional[list[int]] = None) -> AsyncIterator[str]:
+        """Yield the request's output text as it is produced, one delta per
+        step that added text."""
         if sampling_params is None:
             sampling_params = SamplingParams(temperature=0.0, max_tokens=256)
         request_id = await self.add_request(prompt, sampling_params, request_id, prompt_token_ids)
-        queue = self._request_streams[request_id]
+        queue = self._streams[request_id]
+        done = False
         try:
             while True:
                 item = await queue.get()
-                if item is None:
-                    break
+                if item is _END:
+                    done = True
+                    return
+                if isinstance(item, _Failed):
+                    done = True
+                    raise RuntimeError(f"request {request_id} failed in the engine") from item.exc
                 yield item
         finally:
-            self._request_streams.pop(request_id, None)
+            self._streams.pop(request_id, None)
+            if not done and self._thread is not None:
+                self._post("abort", request_id)     # the reader went away
 
     async def generate(self, prompt: str, sampling_params: Optional[SamplingParams] = None) -> str:
         return "".join([d async for d in self.stream(prompt, sampling_params)])
 
-    def _ensure_step_loop(self) -> None:
-        if self._running:
-            return
-        self._running = True
-        self._step_task = asyncio.ensure_future(self._step_loop())
-
-    async def _step_loop(self) -> None:
-        loop = asyncio.get_running_loop()
-        try:
-            while self._engine.has_unfinished():
-                outputs = await loop.run_in_executor(None, self._engine.step)
-                for out in outputs:
-                    queue = self._request_streams.get(out.request_id)
-                    if queue is None:
-                        continue
-                    if out.delta_text:
-                        await queue.put(out.delta_text)
-                    if out.finished:
-                        await queue.put(None)
-                await asyncio.sleep(0)
-        finally:
-            self._running = False
-            self._step_task = None
-
     async def abort(self, request_id: str) -> None:
-        self._engine.scheduler.abort_request(request_id)
-        queue = self._request_streams.pop(request_id, None)
-        if queue is not None:
-            await queue.put(None)
+        """Stop a request; its stream ends once the engine thread applied it."""
+        if self._thread is not None:
+            self._post("abort", request_id)
 
     @property
     def has_unfinished(self) -> bool:
-        return self._engine is not None and self._engine.has_unfinished()
+        eng = self._engine
+        with self._wake:
+            pending = bool(self._inbox)
+        return eng is not None and (pending or eng.has_unfinished())
+
+    # -- engine thread -------------------------------------------------------
+    def _post(self, command: str, payload) -> None:
+        with self._wake:
+            self._inbox.append((command, payload))
+            self._wake.notify()
+
+    def _to_loop(self, fn, *args) -> None:
+        try:
+            self._loop.call_soon_threadsafe(fn, *args)
+        except RuntimeError:      # the event loop is closed: nobody is listening
+            pass
+
+    def _run_engine(self) -> None:
+        eng = self._engine
+        while True:
+            with self._wake:
+                while not self._inbox and not eng.has_unfinished():
+                    self._wake.wait()
+                commands = list(self._inbox)
+                self._inbox.clear()
+            for command, payload in commands:
+                if command == "stop":
+                    return
+                if command == "add":
+                    rid, prompt, params, ids = payload
+                    try:
+                        eng.add_request(prompt, params, rid, prompt_token_ids=ids)
+                    except Exception as exc:       # bad request: only its stream fails
+                        self._to_loop(self._deliver, rid, _Failed(exc))
+                elif command == "abort":
+                    eng.scheduler.abort_request(payload)
+                    self._to_loop(self._deliver, payload, _END)
+            if not eng.has_unfinished():
+                continue
+            try:
+                outputs = eng.step()
+            except BaseException as exc:           # the engine is unusable now
+                self._error = exc
+                self._to_loop(self._fail_all, exc)
+                return
+            if outputs:
+                self._to_loop(self._dispatch, outputs)
+
+    # -- event-loop side -----------------------------------------------------
+    def _deliver(self, request_id: str, item) -> None:
+        queue = self._streams.get(request_id)
+        if queue is not None:
+            queue.put_nowait(item)
+
+    def _dispatch(self, outputs) -> None:
+        for out in outputs:
+            queue = self._streams.get(out.request_id)
+            if queue is None:
+                continue
+            if out.delta_text:
+                queue.put_nowait(out.delta_text)
+            if out.finished:
+                queue.put_nowait(_END)
+
+    def _fail_all(self, exc: BaseException) -> None:
+        for queue in self._streams.values():
+            queue.put_nowait(_Failed(exc))
