@@ -422,7 +422,7 @@ def bench_e2e(args):
     return result
 
 
-def cpu_baseline_e2e(state, model_config, prompts, streams, n_seqs: int = 8, n_steps: int = 4,
+def cpu_baseline_e2e(state, model_config, prompts, streams, n_seqs: int = 8, n_steps: int = 64,
                      margin_bar: float = 0.1):
     """The reference's CPU model path restated (oracle.model, fp32, the same
     random weights): prefill the first n_seqs prompts of the workload

@@ -2,11 +2,15 @@
 compiler under AddressSanitizer and UndefinedBehaviorSanitizer (no GPU):
 the persistent kernel's range split and the piece bookkeeping shared with
 its reduce kernel (tests/host_model/range_split_check.cpp, which includes
-the kernels' own lite-vllm_amd/csrc/lv_split.h), and the oracle's C sampler
-(oracle/sampler_ref.c) driven over edge-case rows."""
+the kernels' own lite-vllm_amd/csrc/lv_split.h), the oracle's C sampler
+(oracle/sampler_ref.c) driven over edge-case rows, and the library's host
+code (workspace sizes against a model of what the kernels address, argument
+checks of every entry point, tests/host_model/capi_host_check.cpp)."""
 
 from __future__ import annotations
 
+import concurrent.futures
+import os
 import shutil
 import subprocess
 from pathlib import Path
@@ -33,3 +37,46 @@ def test_range_split_and_piece_bookkeeping(tmp_path):
     proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert proc.returncode == 0, proc.stderr[-4000:]
     assert "all checks passed" in proc.stdout
+
+
+def test_oracle_sampler_under_sanitizers(tmp_path):
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no gcc")
+    exe = tmp_path / "sampler_ref_check"
+    subprocess.run([gcc, "-std=c11", "-O1", "-g", "-ffp-contract=off", *SAN,
+                    str(HERE / "sampler_ref_check.c"), str(ROOT / "oracle" / "sampler_ref.c"),
+                    "-o", str(exe), "-lm"], check=True)
+    proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0, proc.stderr[-4000:]
+    assert "all passed" in proc.stdout
+
+
+def test_library_host_code_under_sanitizers(tmp_path):
+    """The library's sources compiled host-only (relocatable device code,
+    none of it built, so nothing can launch) with ASan/UBSan on the host
+    side, linked into a driver that checks every workspace-size function
+    against a model of what the kernels address and every entry point's
+    refusal of bad arguments."""
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("no hipcc")
+    host_san = [x for f in SAN for x in ("-Xarch_host", f)]
+    flags = ["--offload-host-only", "-fgpu-rdc", "-O1", "-g", "-fPIC", "-std=c++17",
+             f"-I{ROOT / 'include'}", f"-I{CSRC}", *host_san]
+
+    def compile_one(src: Path) -> Path:
+        obj = tmp_path / (src.stem + ".o")
+        subprocess.run([hipcc, *flags, "-c", str(src), "-o", str(obj)], check=True,
+                       capture_output=True)
+        return obj
+    srcs = sorted(CSRC.glob("*.hip")) + [HERE / "capi_host_check.cpp"]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=8) as ex:
+        objs = list(ex.map(compile_one, srcs))
+    exe = tmp_path / "capi_host_check"
+    subprocess.run([hipcc, "-fgpu-rdc", "--offload-arch=gfx950", *host_san, *map(str, objs),
+                    "-o", str(exe)], check=True, capture_output=True)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0", HIP_VISIBLE_DEVICES="")
+    proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300, env=env)
+    assert proc.returncode == 0, proc.stderr[-4000:]
+    assert "all passed" in proc.stdout
