@@ -479,9 +479,10 @@ def cpu_baseline_e2e(state, model_config, prompts, streams, n_seqs: int = 8, n_s
               "clear_margin_tokens": checked, "argmax_match": exact,
               "max_gap_below_oracle_max": round(max_gap, 4), "bar": margin_bar,
               "ok": exact == checked and max_gap <= margin_bar,
-              "check": "engine tokens of the timed run (prompts 0-7, first 5 tokens) vs the fp32 "
-                       "oracle decoder teacher-forced on them: argmax where the oracle's top-2 "
-                       "margin >= bar, within bar of its max everywhere"}
+              "check": f"engine tokens of the timed run (prompts 0-{n_seqs - 1}, first "
+                       f"{n_steps + 1} tokens) vs the fp32 oracle decoder teacher-forced on them: "
+                       "argmax where the oracle's top-2 margin >= bar, within bar of its max "
+                       "everywhere"}
     return base, parity
 
 
