@@ -182,6 +182,10 @@ def bench_sampler(args):
     sb = workloads.sampler_batch(seed=0)
     logits = sb.logits.to(dev)
     temp = sb.temperature.to(dev)
+    if args.sampler_rows == "greedy":
+        temp = torch.zeros_like(temp)
+    elif args.sampler_rows == "temperature":
+        temp = torch.full_like(temp, 0.75)
     uni = sb.uniform.to(dev)
     out = torch.empty(logits.shape[0], dtype=torch.int64, device=dev)
     total_ms, per = _time_gpu(lambda: ops.sample(logits, temp, uni, out=out), args.steps,
@@ -193,9 +197,12 @@ def bench_sampler(args):
     res = {
         "value": round(B / (kern_ms * 1e-3), 1), "unit": "sampled rows/s",
         "ms_per_step": round(total_ms / args.steps, 4),
-        "config": {"workload": "config4 fused sampler: [256, 151936] bf16 logits N(0,16), "
-                               "rows 0-127 greedy, 128-255 T~U[0.5,1], supplied uniforms",
-                   "kernel": "lv_sample (sampler_segments_kernel + sampler_search_kernel)"},
+        "config": {"workload": ("config4 fused sampler: [256, 151936] bf16 logits N(0,16), "
+                                "rows 0-127 greedy, 128-255 T~U[0.5,1], supplied uniforms"
+                                if args.sampler_rows == "config4" else
+                                f"config4 logits, all rows {args.sampler_rows} (diagnostic)"),
+                   "kernel": "lv_sample (sampler_items_kernel + sampler_finish_kernel; "
+                             "the roofline figures are over the whole call)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": _traffic("sampler"),
@@ -518,6 +525,10 @@ def main() -> int:
     ap.add_argument("--output-len", type=int, default=1024,
                     help="e2e: output tokens per request")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sampler-rows", choices=["config4", "greedy", "temperature"],
+                    default="config4",
+                    help="sampler workload rows: config 4's half/half mix (the bench line), "
+                         "all greedy, or all at T = 0.75 (same logits; a diagnostic)")
     ap.add_argument("--eager", action="store_true",
                     help="e2e: no HIP graphs for decode steps")
     ap.add_argument("--no-secondary", action="store_true",

@@ -272,7 +272,7 @@ int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
  * Arguments, results and errors are those of lv_sample.  Its scratch is a
  * fixed 4 MiB array in the library's device code, one copy per GPU, looked
  * up on the first call on each device; calls needing more than
- * lv_sample_workspace_size(num_rows, vocab_size) <= 4 MiB (e.g. above 1564
+ * lv_sample_workspace_size(num_rows, vocab_size) <= 4 MiB (e.g. above 1765
  * rows at vocab 151936) are rejected with LV_ERR_WORKSPACE.  Every call on a
  * GPU uses that GPU's one copy: calls that overlap on one GPU (two streams,
  * two threads) race.

@@ -1,13 +1,18 @@
 // Fused greedy / temperature sampler over [B, V] logits.
 //
-// Two launches.  sampler_segments_kernel spreads every row over
-// ceil(nseg / SPW) workgroups (SPW = 4 wavefronts x UNROLL segments in
-// flight x GROUPS rounds, one wavefront per segment; default 16):
-// greedy rows leave one (max, index) candidate per workgroup, temperature
-// rows leave (m_s, sigma_s) per segment (defined below).  Each segment's
-// arithmetic is self-contained, so how segments are spread over workgroups
-// does not change any bit.  sampler_search_kernel (one workgroup per row)
-// merges the candidates or runs the cross-segment part and the search.
+// Two launches.  sampler_items_kernel streams the batch as "items" of two
+// consecutive 512-element segments of one row, spread over a grid of a few
+// workgroups per CU: wavefront w takes items w, w + nw, w + 2 nw, ... (nw
+// wavefronts in all), so every wavefront meets the batch's greedy and
+// temperature rows in proportion and neighbouring wavefronts read
+// neighbouring segments.  The next item's loads are issued before the
+// current item is folded.  Per segment it stores the maximum and, for a
+// temperature row, sigma_s (defined below).  Each segment's arithmetic is
+// self-contained, so how items are spread over wavefronts does not change
+// any bit.  sampler_finish_kernel (one wavefront per row) finds a greedy
+// row's first maximum (the first segment holding the row maximum, then its
+// first element equal to it), or runs the cross-segment part and the
+// search of a temperature row.
 //
 // Greedy rows (temperature 0) follow _argmax_kernel / torch.argmax
 // (reference litevllm/layers/sampler.py:60-84, 111-124): the first index of
@@ -40,11 +45,18 @@
 //   level 4: q = A_{k-1} (0 for k = 0); for j in the chunk: q <- q + e_j;
 //            first j with e_j > 0 and base + q * scale > r, else the last j
 //            with e_j > 0.
+//   exp2_det(t), t <= 0 in every use: t < -200 and NaN become -200;
+//            n = floor(t), f = t - n (a result of 1.0, from t in (-2^-25, 0),
+//            becomes the largest float below 1: the fract instruction's
+//            clamp); P(f) = 1 + f(c1 + f(c2 + f(c3 + f(c4 + f c5)))) with
+//            fused multiply-adds, c1..c5 a degree-5 minimax fit of 2^f on
+//            [0, 1) rounded to fp32; result ldexp(P(f), n), rounded once
+//            (subnormal below 2^-126, 0 below about 2^-150).
 // Every sum, product and comparison is an IEEE fp32 operation in the order
-// written (this file is compiled with -ffp-contract=off); exp2_det uses only
-// fmaf, rint and exact power-of-two scaling.
+// written (this file is compiled with -ffp-contract=off).
 #include <stdlib.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -58,30 +70,51 @@ constexpr int kMaxSegs = 4096;  // vocab up to 2^21
 // log2(e) rounded to fp32.
 constexpr float kLog2e = 0x1.715476p+0f;
 
-// exp2 for t <= 0 by range reduction t = n + f, |f| <= 1/2, and the degree-7
-// Taylor polynomial of 2^f = sum_k (f ln2)^k / k! (coefficients ln2^k/k!
-// rounded to fp32) evaluated by Horner with fused multiply-adds; 2^n is
-// applied by an exact power-of-two multiply.  Inputs below -125 (and NaN)
-// give 0, so no result is subnormal.  Relative error < 2^-22 on [-125, 0].
+// exp2_det of the header: fract + floor-convert + five fused multiply-adds
+// + ldexp.  The relative error of P against 2^f is below 2^-22.7 for every
+// fp32 f in [0, 1), and P(0) = 1, so exp2_det(0) = 1 exactly.
 __device__ __forceinline__ float exp2_det(float t) {
-  // Branch-free form of: t < -125 or NaN -> 0; t > 0 -> t = 0.  For t in
-  // [-125, 0] the clamps leave t unchanged, so every result equals the
-  // plain definition above bit for bit.
-  const bool under = !(t >= -125.0f);
-  t = fmaxf(fminf(t, 0.0f), -125.0f);
-  const float n = rintf(t);
-  const float f = t - n;  // exact (Sterbenz)
-  float p = 0x1.ffcbfcp-17f;
-  p = fmaf(p, f, 0x1.430912p-13f);
-  p = fmaf(p, f, 0x1.5d87fep-10f);
-  p = fmaf(p, f, 0x1.3b2ab6p-7f);
-  p = fmaf(p, f, 0x1.c6b08ep-5f);
-  p = fmaf(p, f, 0x1.ebfbep-3f);
-  p = fmaf(p, f, 0x1.62e43p-1f);
-  p = fmaf(p, f, 1.0f);
-  const int ni = (int)n;
-  const float scale = __uint_as_float((uint32_t)(ni + 127) << 23);
-  return under ? 0.0f : p * scale;
+  t = fmaxf(t, -200.0f);                      // NaN -> -200
+  const float f = __builtin_amdgcn_fractf(t);  // t - floor(t), clamped below 1
+  int n;
+  asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(n) : "v"(t));
+  float q = 0x1.e974fap-10f;
+  q = fmaf(q, f, 0x1.277856p-7f);
+  q = fmaf(q, f, 0x1.c91ce6p-5f);
+  q = fmaf(q, f, 0x1.ebdb5ap-3f);
+  q = fmaf(q, f, 0x1.62e4bap-1f);
+  const float p = fmaf(q, f, 1.0f);
+  return __builtin_amdgcn_ldexpf(p, n);
+}
+
+// Maximum over the 64 lanes, every lane receiving it.  The four in-row steps
+// are DPP max instructions written out (lane i with i^1, i^2, 7-i within 8,
+// 15-i within 16); the inputs are fmaxf results, hence never signalling
+// NaNs, so no canonicalizing step is needed between them.  The cross-row
+// steps go through the LDS crossbar.
+__device__ __forceinline__ float wave_max64(float x) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1"
+      : "+v"(x));
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
+// Maximum of a lane's 8 elements.
+__device__ __forceinline__ float max8(const float x[8]) {
+  float m = fmaxf(fmaxf(x[0], x[1]), x[2]);
+  m = fmaxf(fmaxf(m, x[3]), x[4]);
+  m = fmaxf(fmaxf(m, x[5]), x[6]);
+  return fmaxf(m, x[7]);
 }
 
 // Load elements [512 s + 8 lane, +8) of a row as fp32; entries past V are
@@ -115,177 +148,242 @@ __device__ __forceinline__ float wave_scan_hs(float a, int lane) {
 }
 
 // Per-chunk exp weights and their sequential sum (the a_k of the header).
+// The sum starts from e_0 itself: 0 + e_0 = e_0, as e_0 >= +0.
 __device__ __forceinline__ float chunk_weights(const float x[8], float ms, float c, float e[8]) {
-  float a = 0.0f;
+  e[0] = exp2_det((x[0] - ms) * c);
+  float a = e[0];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 1; j < 8; ++j) {
     e[j] = exp2_det((x[j] - ms) * c);
     a = a + e[j];
   }
   return a;
 }
 
-__device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi) {
-  return v > bv || (v == bv && i < bi);
-}
-
-constexpr int kSegThreads = 256;
-constexpr int kSegWaves = kSegThreads / 64;
-
-
+// Per-(row, segment) results of the first kernel, [rows, nseg] each:
+// m = the segment's maximum (fp32, NaN ignored); w = sigma_s (temperature
+// rows; 0 for greedy rows).
 struct SampWs {
-  float* m;        // [rows, nseg] segment maxima
-  float* w;        // [rows, nseg] segment sums sigma_s
-  float* bv;       // [rows, split] greedy candidates: value
-  int64_t* bi;     //                                  index
+  float* m;
+  float* w;
 };
 
-template <typename T, int UNROLL, int GROUPS>
-__global__ __launch_bounds__(kSegThreads) void sampler_segments_kernel(
-    const T* __restrict__ logits, int64_t V, int64_t row_stride,
-    const float* __restrict__ temperature, SampWs ws, int nseg, int split, int vec_ok) {
-  constexpr int kUnroll = UNROLL, kGroups = GROUPS;
-  constexpr int kSegsPerWG = kSegWaves * kUnroll * kGroups;
-  __shared__ float s_gv[kSegWaves];
-  __shared__ int64_t s_gi[kSegWaves];
-  const int64_t r = blockIdx.x;
-  const int part = blockIdx.y;
-  const T* row = logits + r * row_stride;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const bool vec = vec_ok != 0;
-  const float temp = temperature[r];
-  const float c = kLog2e / temp;
-  const bool greedy = !(temp > 0.0f) || !(c <= 3.0e38f);
-  const int sbeg = part * kSegsPerWG;
-  const int send = min(nseg, sbeg + kSegsPerWG);
+constexpr int kItemSegs = 2;               // segments per item
+constexpr int kItemWaves = 4;              // wavefronts per workgroup
+constexpr int kItemThreads = 64 * kItemWaves;
+constexpr int kMaxItemsPerWave = 64;       // lane k holds the k-th item's c
 
-  // Wavefront w folds segments sbeg + w + 4 i in groups of UNROLL; segment
-  // index of group g, slot u: sbeg + w + 4 (UNROLL g + u).
-  auto seg_of = [&](int g, int u) { return sbeg + wave + kSegWaves * (kUnroll * g + u); };
-  auto load_group = [&](int g, float (*x)[8]) {
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int s = seg_of(g, u);
-      if (s < send) load_chunk(row, V, s, lane, vec, x[u]);
-    }
-  };
-  float xa[kUnroll][8], xb[kUnroll][8];
-  if (greedy) {
-    float bv = -__builtin_inff();
-    int64_t bi = INT64_MAX;
-    auto fold = [&](int g, float (*x)[8]) {
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int s = seg_of(g, u);
-        if (s < send) {
-          const int64_t e0 = (int64_t)s * kSeg + lane * 8;
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            if (x[u][j] > bv) { bv = x[u][j]; bi = e0 + j; }
-        }
-      }
-    };
-    load_group(0, xa);
-#pragma unroll
-    for (int g = 0; g < kGroups; g += 2) {
-      if (g + 1 < kGroups) load_group(g + 1, xb);
-      fold(g, xa);
-      if (g + 2 < kGroups) load_group(g + 2, xa);
-      if (g + 1 < kGroups) fold(g + 1, xb);
-    }
-    // Lanes may hold their best from a later segment than an equal value of
-    // another lane, so merges are lexicographic on (value, index).
-#pragma unroll
-    for (int ofs = 32; ofs >= 1; ofs >>= 1) {
-      const float ov = __shfl_xor(bv, ofs);
-      const int64_t oi = __shfl_xor(bi, ofs);
-      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
-    if (lane == 0) { s_gv[wave] = bv; s_gi[wave] = bi; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      for (int w = 1; w < kSegWaves; ++w)
-        if (better(s_gv[w], s_gi[w], bv, bi)) { bv = s_gv[w]; bi = s_gi[w]; }
-      ws.bv[r * split + part] = bv;
-      ws.bi[r * split + part] = bi;
-    }
-    return;
+// One lane's 8 elements of a segment, fetched in one step and converted in
+// another so the loads stay in flight while the previous item is folded.
+// VEC (16-byte aligned rows, V % 8 == 0): 16-byte loads (two for fp32) at
+// a byte offset clamped into the row; a lane chunk is then either wholly
+// inside the row or wholly past V, and the fold masks the latter.
+template <typename T, bool VEC>
+struct SegWords {
+  static constexpr int kWords = elem<T>::kPer16B == 8 ? 1 : 2;
+  uint4 w[kWords];
+
+  __device__ __forceinline__ void fetch(const T* __restrict__ row, int V, int sg,
+                                        uint32_t lane_bytes) {
+    // lane_bytes = 0 for every lane (a placeholder fetch) reads one line
+    const uint32_t lim = (uint32_t)(V - 8 - sg * kSeg) * (uint32_t)sizeof(T);
+    const char* p = (const char*)row + (uint32_t)sg * (kSeg * (uint32_t)sizeof(T)) +
+                    min(lane_bytes, lim);
+    w[0] = load16_nt(p);
+    if constexpr (kWords == 2) w[1] = load16_nt(p + 16);
   }
-  // Per-segment max and scanned exp weights.
-  auto fold = [&](int g, float (*x)[8]) {
+  __device__ __forceinline__ void unpack(float x[8]) const {
+    elem<T>::unpack(w[0], x);
+    if constexpr (kWords == 2) elem<T>::unpack(w[1], x + 4);
+  }
+};
+
+// General rows: guarded element loads, converted at once (entries past V
+// are -inf already).
+template <typename T>
+struct SegWords<T, false> {
+  float v[8];
+
+  __device__ __forceinline__ void fetch(const T* __restrict__ row, int V, int sg,
+                                        uint32_t lane_bytes) {
+    const int e0 = sg * kSeg + (int)(lane_bytes / sizeof(T));
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int s = seg_of(g, u);
-      if (s < send) {
+    for (int j = 0; j < 8; ++j) v[j] = (e0 + j < V) ? elem<T>::load(row + e0 + j) : -__builtin_inff();
+  }
+  __device__ __forceinline__ void unpack(float x[8]) const {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = v[j];
+  }
+};
+
+// Grid requirements (sample_launch): rows * ceil(nseg / 2) < 2^31, rows *
+// nseg < 2^31, and at most kMaxItemsPerWave items per wavefront.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kItemThreads) void sampler_items_kernel(
+    const T* __restrict__ logits, int V, int64_t row_stride,
+    const float* __restrict__ temperature, SampWs ws, int rows, int nseg) {
+  const int lane = threadIdx.x & 63;
+  const int w = blockIdx.x * kItemWaves + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int nw = gridDim.x * kItemWaves;
+  const int ipr = (nseg + kItemSegs - 1) / kItemSegs;   // items per row
+  const int total = rows * ipr;
+  if (w >= total) return;
+  // Lane k: c of the wavefront's item k (w + k nw), or -1 for a greedy row;
+  // one division per wavefront instead of one per item.
+  float cv;
+  {
+    const int ik = min(w + lane * nw, total - 1);
+    const float temp = temperature[ik / ipr];
+    const float c = kLog2e / temp;
+    cv = (!(temp > 0.0f) || !(c <= 3.0e38f)) ? -1.0f : c;
+  }
+  const uint32_t lane_bytes = (uint32_t)lane * 8u * (uint32_t)sizeof(T);
+  // fetch(i, live = false) is the placeholder issued past the wavefront's
+  // last item: every lane reads the first 16 bytes of item i's row (one
+  // cache line, no HBM stream), so the loop's loads stay unconditional.
+  auto fetch = [&](int i, bool live, SegWords<T, VEC>* b) {
+    const int r = i / ipr;
+    const int s0 = live ? (i - r * ipr) * kItemSegs : 0;
+    const uint32_t lb = live ? lane_bytes : 0u;
+    const T* row = logits + (int64_t)r * row_stride;
+#pragma unroll
+    for (int u = 0; u < kItemSegs; ++u) b[u].fetch(row, V, min(s0 + u, nseg - 1), lb);
+  };
+  auto fold = [&](int i, int k, const SegWords<T, VEC>* b) {
+    const int r = i / ipr;
+    const int s0 = (i - r * ipr) * kItemSegs;
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), k));
+    const bool greedy = c < 0.0f;
+    float mres[kItemSegs], wres[kItemSegs];
+#pragma unroll
+    for (int u = 0; u < kItemSegs; ++u) {
+      float x[8];
+      b[u].unpack(x);
+      if ((s0 + u + 1) * kSeg > V) {   // uniform: the row's last segment (or past it)
+        const bool past = (s0 + u) * kSeg + lane * 8 >= V;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = past ? -__builtin_inff() : x[j];
+      }
+      const float ms = wave_max64(max8(x));
+      mres[u] = ms;
+      wres[u] = 0.0f;
+      if (!greedy) {
+        // sigma_s = A_63 of the header's Hillis-Steele scan.  The butterfly
+        // sum adds the same pairs in the same order (lane 63 holds the
+        // larger index of every pair, as in A_k + A_{k-d}; fp32 addition is
+        // commutative, so every lane ends with A_63's bits).
         float e[8];
-        float ms = x[u][0];
-#pragma unroll
-        for (int j = 1; j < 8; ++j) ms = fmaxf(ms, x[u][j]);
-        ms = group_max<64>(ms);
-        const float A = wave_scan_hs(chunk_weights(x[u], ms, c, e), lane);
-        if (lane == 63) {
-          ws.m[r * nseg + s] = ms;
-          ws.w[r * nseg + s] = A;
-        }
+        wres[u] = group_sum<64>(chunk_weights(x, ms, c, e));
       }
     }
-  };
-  load_group(0, xa);
+    // Lane l stores slot l % 4 (m of segment s0 + slot, or sigma of segment
+    // s0 + slot - 2); every lane stores, so no store sits under a branch and
+    // the compiler keeps counting the next item's loads instead of waiting
+    // for them.  A slot past the row's last segment repeats that segment's
+    // store.
+    const int slot = lane & (2 * kItemSegs - 1);
+    const int uu = min(slot < kItemSegs ? slot : slot - kItemSegs, nseg - 1 - s0);
+    float vm = mres[0], vw = wres[0];
 #pragma unroll
-  for (int g = 0; g < kGroups; g += 2) {
-    if (g + 1 < kGroups) load_group(g + 1, xb);
-    fold(g, xa);
-    if (g + 2 < kGroups) load_group(g + 2, xa);
-    if (g + 1 < kGroups) fold(g + 1, xb);
+    for (int u = 1; u < kItemSegs; ++u) {
+      vm = (uu == u) ? mres[u] : vm;
+      vw = (uu == u) ? wres[u] : vw;
+    }
+    float* dst = (slot < kItemSegs ? ws.m : ws.w) + (r * nseg + s0 + uu);
+    *dst = slot < kItemSegs ? vm : vw;
+  };
+  // Two items in flight.  Past the wavefront's last item the prefetch is a
+  // placeholder; the empty asm and the scheduling barrier keep each
+  // prefetch above the fold that follows it.
+  SegWords<T, VEC> ba[kItemSegs], bb[kItemSegs];
+  int i = w, k = 0;
+  fetch(i, true, ba);
+  for (;;) {
+    const int i1 = i + nw;
+    const bool more1 = i1 < total;
+    fetch(more1 ? i1 : i, more1, bb);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    fold(i, k, ba);
+    if (!more1) break;
+    const int i2 = i1 + nw;
+    const bool more2 = i2 < total;
+    fetch(more2 ? i2 : i1, more2, ba);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    fold(i1, k + 1, bb);
+    if (!more2) break;
+    i = i2;
+    k += 2;
   }
 }
 
+// One wavefront per row: merge the greedy candidates, or run the
+// cross-segment scan and the four-level search of the header.
 template <typename T>
-__global__ __launch_bounds__(kSegThreads) void sampler_search_kernel(
+__global__ __launch_bounds__(64) void sampler_finish_kernel(
     const T* __restrict__ logits, int64_t V, int64_t row_stride,
     const float* __restrict__ temperature, const float* __restrict__ uniform, SampWs ws,
-    int nseg, int split, int64_t* __restrict__ out, int vec_ok) {
-  __shared__ float s_m[kMaxSegs];
-  __shared__ float s_w[kMaxSegs];
+    int nseg, int64_t* __restrict__ out, int vec_ok) {
+  extern __shared__ float s_mw[];   // segment maxima [nseg], then weights [nseg]
+  float* s_m = s_mw;
+  float* s_w = s_mw + nseg;
   const int64_t r = blockIdx.x;
   const T* row = logits + r * row_stride;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x;
   const bool vec = vec_ok != 0;
   const float temp = temperature[r];
+  const float u = uniform[r];
+  // The workspace rows go to LDS while the temperature load is in flight
+  // (both kinds of row read the maxima).
+  const float* wm = ws.m + r * nseg;
+  const float* ww = ws.w + r * nseg;
+  for (int i = lane; i < nseg; i += 64) {
+    s_m[i] = wm[i];
+    s_w[i] = ww[i];
+  }
+  __syncthreads();
   const float c = kLog2e / temp;
   const bool greedy = !(temp > 0.0f) || !(c <= 3.0e38f);
   if (greedy) {
-    if (threadIdx.x == 0) {
-      float bv = -__builtin_inff();
-      int64_t bi = INT64_MAX;
-      for (int p = 0; p < split; ++p)
-        if (better(ws.bv[r * split + p], ws.bi[r * split + p], bv, bi)) {
-          bv = ws.bv[r * split + p];
-          bi = ws.bi[r * split + p];
-        }
-      out[r] = (bi == INT64_MAX) ? 0 : bi;
+    // the first index of the row maximum: the first segment whose maximum
+    // is the row's, then the first element there equal to it (NaN never
+    // wins; a row with nothing above -inf gives 0)
+    float M = -__builtin_inff();
+    for (int sg = lane; sg < nseg; sg += 64) M = fmaxf(M, s_m[sg]);
+    M = group_max<64>(M);
+    if (!(M > -__builtin_inff())) {
+      if (lane == 0) out[r] = 0;
+      return;
     }
+    int first = nseg;
+    for (int sg = lane; sg < nseg; sg += 64)
+      if (s_m[sg] == M) { first = sg; break; }
+#pragma unroll
+    for (int ofs = 32; ofs >= 1; ofs >>= 1) first = min(first, __shfl_xor(first, ofs));
+    float x[8];
+    load_chunk(row, V, first, lane, vec, x);
+    int j = 8;
+#pragma unroll
+    for (int jj = 7; jj >= 0; --jj)
+      if (x[jj] == M) j = jj;
+    const uint64_t hit = __ballot(j < 8);
+    const int kk = hit ? __ffsll((unsigned long long)hit) - 1 : 0;
+    const int jk = __shfl(j, kk);
+    if (lane == 0) out[r] = (int64_t)first * kSeg + kk * 8 + (jk < 8 ? jk : 0);
     return;
   }
-  for (int i = threadIdx.x; i < nseg; i += kSegThreads) {
-    s_m[i] = ws.m[r * nseg + i];
-    s_w[i] = ws.w[r * nseg + i];
-  }
-  __syncthreads();
-  if (wave != 0) return;
 
-  // Phase 2 (one wavefront): segment weights, total and the search.
+  // Segment weights, total and the search.
   float M = -__builtin_inff();
-  for (int s = lane; s < nseg; s += 64) M = fmaxf(M, s_m[s]);
+  for (int sg = lane; sg < nseg; sg += 64) M = fmaxf(M, s_m[sg]);
   M = group_max<64>(M);
   const int R = (nseg + 63) / 64;
   const int g0 = min(nseg, lane * R), g1 = min(nseg, g0 + R);
   float b = 0.0f;
-  for (int s = g0; s < g1; ++s) {
-    const float w = s_w[s] * exp2_det((s_m[s] - M) * c);
-    s_w[s] = w;  // each lane owns its own segments
+  for (int sg = g0; sg < g1; ++sg) {
+    const float w = s_w[sg] * exp2_det((s_m[sg] - M) * c);
+    s_w[sg] = w;  // each lane owns its own segments
     b = b + w;
   }
   const float B = wave_scan_hs(b, lane);
@@ -294,7 +392,6 @@ __global__ __launch_bounds__(kSegThreads) void sampler_search_kernel(
     if (lane == 0) out[r] = 0;
     return;
   }
-  const float u = uniform[r];
   const float target = u * S;
 
   // Level 1.
@@ -315,17 +412,17 @@ __global__ __launch_bounds__(kSegThreads) void sampler_search_kernel(
   float base = 0.0f;
   {
     float acc = base_k;
-    for (int s = t0; s < t1; ++s) {
-      const float w = s_w[s];
+    for (int sg = t0; sg < t1; ++sg) {
+      const float w = s_w[sg];
       const float nxt = acc + w;
-      if (nxt > target) { sstar = s; base = acc; break; }
+      if (nxt > target) { sstar = sg; base = acc; break; }
       acc = nxt;
     }
     if (sstar < 0) {
       acc = base_k;
-      for (int s = t0; s < t1; ++s) {
-        const float w = s_w[s];
-        if (w > 0.0f) { sstar = s; base = acc; }
+      for (int sg = t0; sg < t1; ++sg) {
+        const float w = s_w[sg];
+        if (w > 0.0f) { sstar = sg; base = acc; }
         acc = acc + w;
       }
     }
@@ -377,21 +474,37 @@ __global__ __launch_bounds__(kSegThreads) void sampler_search_kernel(
 }  // namespace lv
 
 namespace lv {
-// Segments per workgroup of the first kernel (LV_SAMPLER_SPW = 4, 8, 16,
-// 32: a tuning knob; 16 measured best on config 4).
-static inline int samp_spw() {
-  static const int v = [] {
-    const char* e = getenv("LV_SAMPLER_SPW");
-    const int x = e ? atoi(e) : 16;
-    return (x == 4 || x == 8 || x == 16 || x == 32) ? x : 16;
-  }();
-  return v;
-}
-static inline int64_t samp_split(int nseg) { return (nseg + samp_spw() - 1) / samp_spw(); }
+// Workspace: per (row, segment) two floats, 256-byte aligned.
 static inline size_t samp_ws_bytes(int64_t rows, int64_t V) {
   const int64_t nseg = (V + kSeg - 1) / kSeg;
-  const int64_t split = samp_split((int)nseg);
-  return (size_t)rows * (size_t)(split * 16 + nseg * 8) + 256;
+  return (size_t)rows * (size_t)nseg * 8 + 256;
+}
+
+// Workgroups of the item kernel for `items` items: LV_SAMPLER_WGS_PER_CU
+// (default 8, i.e. eight wavefronts per SIMD) per CU, no more wavefronts
+// than items, and enough wavefronts that none has more than
+// kMaxItemsPerWave items.
+static int samp_grid(int64_t items) {
+  static std::atomic<int> cus{0};
+  int n = cus.load(std::memory_order_relaxed);
+  if (n <= 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus.store(n, std::memory_order_relaxed);
+  }
+  static const int per_cu = [] {
+    const char* e = getenv("LV_SAMPLER_WGS_PER_CU");
+    const int v = e ? atoi(e) : 8;
+    return (v >= 1 && v <= 32) ? v : 8;
+  }();
+  const int64_t by_items = (items + kItemWaves - 1) / kItemWaves;
+  const int64_t at_least =
+      (items + (int64_t)kMaxItemsPerWave * kItemWaves - 1) / ((int64_t)kMaxItemsPerWave * kItemWaves);
+  return (int)std::max<int64_t>(at_least,
+                                std::min<int64_t>((int64_t)n * per_cu, std::max<int64_t>(1, by_items)));
 }
 }  // namespace lv
 
@@ -410,35 +523,31 @@ static int sample_launch(const void* logits_dev, int64_t num_rows, int64_t vocab
                          lv_dtype dtype, hipStream_t st) {
   const int vec = aligned16(logits_dev) && ((row_stride * (int64_t)dtype_size(dtype)) % 16 == 0);
   const int nseg = (int)((vocab_size + kSeg - 1) / kSeg);
-  const int split = (int)samp_split(nseg);
   SampWs ws;
-  ws.bi = (int64_t*)base;
-  ws.bv = (float*)(base + (size_t)num_rows * split * 8);
-  ws.m = (float*)(base + (size_t)num_rows * split * 12);
+  ws.m = (float*)base;
   ws.w = ws.m + (size_t)num_rows * nseg;
-  const dim3 grid_a((unsigned)num_rows, (unsigned)split), grid_b((unsigned)num_rows);
-  const dim3 block(kSegThreads);
-#define LV_SEG(TT, U, G)                                                                        \
-  hipLaunchKernelGGL((sampler_segments_kernel<TT, U, G>), grid_a, block, 0, st,                 \
-                     (const TT*)logits_dev, vocab_size, row_stride, temperature_dev, ws, nseg,   \
-                     split, vec)
+  const int64_t items = num_rows * ((nseg + kItemSegs - 1) / kItemSegs);
+  const int grid = samp_grid(items);
+  const bool vec_items = vec && vocab_size % 8 == 0;
 #define LV_SAMPLE_LAUNCH(TT)                                                                    \
-  switch (samp_spw()) {                                                                         \
-    case 4: LV_SEG(TT, 1, 1); break;                                                            \
-    case 8: LV_SEG(TT, 2, 1); break;                                                            \
-    case 32: LV_SEG(TT, 4, 2); break;                                                           \
-    default: LV_SEG(TT, 4, 1); break;                                                           \
-  }                                                                                             \
-  hipLaunchKernelGGL(sampler_search_kernel<TT>, grid_b, block, 0, st, (const TT*)logits_dev,    \
-                     vocab_size, row_stride, temperature_dev, uniform_dev, ws, nseg, split,      \
-                     out_ids_dev, vec)
+  if (vec_items)                                                                                \
+    hipLaunchKernelGGL((sampler_items_kernel<TT, true>), dim3(grid), dim3(kItemThreads), 0, st, \
+                       (const TT*)logits_dev, (int)vocab_size, row_stride, temperature_dev, ws,  \
+                       (int)num_rows, nseg);                                                     \
+  else                                                                                          \
+    hipLaunchKernelGGL((sampler_items_kernel<TT, false>), dim3(grid), dim3(kItemThreads), 0,    \
+                       st, (const TT*)logits_dev, (int)vocab_size, row_stride, temperature_dev,  \
+                       ws, (int)num_rows, nseg);                                                 \
+  hipLaunchKernelGGL(sampler_finish_kernel<TT>, dim3((unsigned)num_rows), dim3(64),              \
+                     sizeof(float) * 2 * (size_t)nseg, st,                                       \
+                     (const TT*)logits_dev, vocab_size, row_stride, temperature_dev,             \
+                     uniform_dev, ws, nseg, out_ids_dev, vec)
   switch (dtype) {
     case LV_BF16: LV_SAMPLE_LAUNCH(bf16); break;
     case LV_F16: LV_SAMPLE_LAUNCH(f16); break;
     default: LV_SAMPLE_LAUNCH(float); break;
   }
 #undef LV_SAMPLE_LAUNCH
-#undef LV_SEG
   return check_launch("sampler kernels");
 }
 
@@ -452,6 +561,8 @@ static int sample_check(const void* logits_dev, int64_t num_rows, int64_t vocab_
   LV_REQUIRE(vocab_size >= 1 && vocab_size <= (int64_t)kSeg * kMaxSegs,
              "lv_sample: vocab_size=%lld outside [1, %d]", (long long)vocab_size, kSeg * kMaxSegs);
   LV_REQUIRE(row_stride >= vocab_size, "lv_sample: row_stride < vocab_size");
+  LV_REQUIRE(num_rows * ((vocab_size + kSeg - 1) / kSeg) <= 0x7fffffff,
+             "lv_sample: num_rows x segments of 512 above 2^31 - 1");
   LV_REQUIRE(logits_dev && temperature_dev && out_ids_dev, "lv_sample: null pointer");
   LV_REQUIRE(uniform_dev, "lv_sample: uniform draws required (pass zeros for all-greedy rows)");
   return LV_OK;

@@ -27,27 +27,26 @@
 #define SEG 512
 #define LANES 64
 
-/* 2^t for t <= 0: t = n + f, |f| <= 1/2; degree-7 Taylor polynomial of
- * 2^f with coefficients ln2^k / k! rounded to fp32, Horner with fmaf;
- * exact power-of-two scaling; t < -125 or NaN -> 0. */
+/* exp2_det(t) for t <= 0 (every use): t < -200 and NaN are first replaced
+ * by -200; n = floor(t), f = t - n (one IEEE subtraction; a result of 1.0,
+ * which only t in (-2^-25, 0) can give, becomes the largest float below 1,
+ * as the GPU's fract instruction clamps it); P(f) = 1 + f (c1 + f (c2 +
+ * f (c3 + f (c4 + f c5)))) by fused multiply-adds, with c1..c5 a degree-5
+ * minimax fit of 2^f on [0, 1) rounded to fp32; result ldexp(P(f), n), one
+ * rounding (subnormal for n < -126, 0 below about -150).  Max relative error
+ * over [-125, 0] < 2^-22.7 (every fp32 f in [0, 1) checked). */
 float oracle_exp2_det(float t) {
-  if (!(t >= -125.0f)) return 0.0f;
-  if (t > 0.0f) t = 0.0f;
-  const float n = rintf(t);
-  const float f = t - n;
-  float p = 0x1.ffcbfcp-17f;
-  p = fmaf(p, f, 0x1.430912p-13f);
-  p = fmaf(p, f, 0x1.5d87fep-10f);
-  p = fmaf(p, f, 0x1.3b2ab6p-7f);
-  p = fmaf(p, f, 0x1.c6b08ep-5f);
-  p = fmaf(p, f, 0x1.ebfbep-3f);
-  p = fmaf(p, f, 0x1.62e43p-1f);
-  p = fmaf(p, f, 1.0f);
-  const int ni = (int)n;
-  uint32_t bits = (uint32_t)(ni + 127) << 23;
-  float scale;
-  memcpy(&scale, &bits, sizeof scale);
-  return p * scale;
+  t = fmaxf(t, -200.0f); /* NaN -> -200 */
+  const float n = floorf(t);
+  float f = t - n;
+  if (f >= 1.0f) f = 0x1.fffffep-1f;
+  float q = 0x1.e974fap-10f;
+  q = fmaf(q, f, 0x1.277856p-7f);
+  q = fmaf(q, f, 0x1.c91ce6p-5f);
+  q = fmaf(q, f, 0x1.ebdb5ap-3f);
+  q = fmaf(q, f, 0x1.62e4bap-1f);
+  const float p = fmaf(q, f, 1.0f);
+  return ldexpf(p, (int)n);
 }
 
 /* In-place inclusive Hillis-Steele scan of 64 values: for d = 1, 2, ..., 32

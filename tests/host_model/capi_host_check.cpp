@@ -6,9 +6,9 @@
 //     skips [2B + 1] ints, two boundary slots per workgroup of (m, l) and
 //     D floats per query head, at up to 4 x the CU count workgroups; the
 //     per-row kernel: one partial per 256-token partition; the prefix pass:
-//     16 splits of (m, l) + D floats per row and head; the sampler:
-//     per-row segment (max, sum) and greedy candidates), over batch sizes
-//     1..7000, heads, head dims and table widths;
+//     16 splits of (m, l) + D floats per row and head; the sampler: a
+//     (maximum, sigma) pair per (row, 512-element segment)), over
+//     batch sizes 1..7000, heads, head dims and table widths;
 //   * that each entry point refuses bad arguments (null pointers, negative
 //     or oversized counts, misaligned buffers, short workspaces) on the host
 //     with the documented status, before anything is enqueued.
@@ -79,9 +79,9 @@ int main() {
   CHECK(lv_paged_attention_prefix_workspace_size(0, 16, 128) == 0, "empty prefix workspace");
   const int64_t vocabs[] = {1, 7, 511, 512, 513, 32000, 151936, 1 << 21};
   for (int64_t V : vocabs)
-    for (int64_t B : {1, 40, 256, 1564, 4096}) {
-      const int64_t nseg = (V + 511) / 512, split = (nseg + 15) / 16;
-      const size_t want = (size_t)B * (size_t)(split * 16 + nseg * 8) + 256;
+    for (int64_t B : {1, 40, 256, 1765, 4096}) {
+      const int64_t nseg = (V + 511) / 512;      // (maximum, sigma) per (row, segment)
+      const size_t want = (size_t)B * (size_t)(nseg * 8) + 256;
       CHECK(lv_sample_workspace_size(B, V) == want, "sampler workspace B=%lld V=%lld",
             (long long)B, (long long)V);
     }

@@ -25,11 +25,14 @@ def test_reference_planted_max_kat():
     kat = KATS["top_k_planted"]
     x = np.zeros((1, kat["vocab"]), dtype=np.float32)
     x[0, kat["planted_index"]] = kat["planted_value"]
-    # greedy and T=1 sampling both land on the planted token (its
-    # probability is 1 - 7e-43, the rest underflow)
+    # greedy and T=1 sampling both land on the planted token: the others
+    # have probability 2^-144.3 each (subnormal in fp32, as exp(-100) is in
+    # the reference's fp32 softmax), so every u above 7 * 2^-144.3 draws it
     assert sampler.sample(x, np.zeros(1, np.float32), np.zeros(1, np.float32)).tolist() == kat["expected"]
-    for u in (0.0, 0.5, 0.999999):
+    for u in (1e-30, 0.5, 0.999999):
         assert sampler.sample(x, np.ones(1, np.float32), np.array([u], np.float32)).tolist() == kat["expected"]
+    # u = 0 is the inverse CDF at 0: the first token of nonzero probability
+    assert sampler.sample(x, np.ones(1, np.float32), np.zeros(1, np.float32)).tolist() == [0]
 
 
 def test_greedy_first_index_on_ties():
@@ -38,12 +41,23 @@ def test_greedy_first_index_on_ties():
 
 
 def test_exp2_det_accuracy():
-    t = np.linspace(-125.0, 0.0, 400001, dtype=np.float32)
+    # normal results: relative error against float64 exp2, including inputs
+    # just below 0 (where t - floor(t) rounds to 1 and is clamped) and tiny
+    # subnormal inputs
+    t = np.concatenate([np.linspace(-125.0, 0.0, 400001, dtype=np.float32),
+                        np.array([-1e-9, -2.0 ** -26, -2.0 ** -24, -1e-30, -1e-45, -0.0,
+                                  -1.0, -0.5, -124.999], np.float32)])
     got = sampler.exp2_det(t).astype(np.float64)
     ref = np.exp2(t.astype(np.float64))
     assert (np.abs(got - ref) / ref).max() < 2.0 ** -22
-    assert sampler.exp2_det(np.array([0.0, -126.0, -np.inf, np.nan], np.float32)).tolist() == \
-        [1.0, 0.0, 0.0, 0.0]
+    # exact powers of two below the normal range (P(0) = 1), gradual
+    # underflow, and the inputs that give 0
+    got = sampler.exp2_det(np.array([0.0, -126.0, -149.0, -150.0, -151.0, -200.0, -1e30,
+                                     -np.inf, np.nan], np.float32)).tolist()
+    assert got == [1.0, 2.0 ** -126, 2.0 ** -149, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0]
+    # between -150 and -126 the result is 2^t rounded to the subnormal grid
+    t = np.float32(-140.3)
+    assert abs(sampler.exp2_det(np.array([t]))[0] - 2.0 ** -140.3) <= 2.0 ** -150
 
 
 def _softmax64(x, T):
@@ -103,11 +117,12 @@ def test_special_cases():
     # tiny temperature -> argmax; huge margin -> that token
     assert one(x, 1e-3, 0.5) == int(np.argmax(x))
     z = np.zeros(V, np.float32)
-    z[517] = 100.0   # every other weight is 2^-144 -> exactly 0
+    z[517] = 110.0   # every other weight is 2^-158.7 -> exactly 0
     for u in (0.0, 0.3, 0.9999):
         assert one(z, 1.0, u) == 517
-    z[517] = 80.0    # others keep 2^-115 > 0: u = 0 picks the first of them
-    assert one(z, 1.0, 0.0) == 0 and one(z, 1.0, 0.3) == 517
+    for big in (100.0, 80.0):   # others keep 2^-144.3 (subnormal) / 2^-115.4 > 0:
+        z[517] = big            # u = 0 picks the first of them
+        assert one(z, 1.0, 0.0) == 0 and one(z, 1.0, 0.3) == 517
     # uniform logits: token = floor(u * V) away from edges
     flat = np.zeros(V, np.float32)
     for u in (0.1234, 0.5, 0.77777):
