@@ -434,6 +434,9 @@ __device__ __forceinline__ i16x4_t lds_read_tr16(const uint16_t* p) {
 
 // Arguments of the MFMA attention body (prefill chunks or shared-prefix
 // units).
+// Chunk sequences a chunk workgroup ranks by length (more: index order).
+constexpr int kChunkRankMax = 256;
+
 template <typename T>
 struct ChunkArgs {
   const T* __restrict__ q; int64_t q_stride;
@@ -445,7 +448,8 @@ struct ChunkArgs {
 };
 
 // PFX = false: prefill chunks (causal, normalised output rows); `unit` is
-// the workgroup id.  PFX = true: one shared-prefix unit -- `unit` is the
+// the workgroup id and `kvh_sel` the chunk sequence (index from seq_begin)
+// the caller's longest-first order gives it.  PFX = true: one shared-prefix unit -- `unit` is the
 // work item, `kvh_sel` the kv head: up to QT group members against one
 // 128-key split of the group's prefix (no causal mask; every prefix key
 // precedes every member's query), writing prefix partials.
@@ -482,12 +486,14 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
   const float scale_log2 = A.scale_log2;
   const PrefixArgs& pfx = A.pfx;
 
-  // XCD-aware order (chunks): workgroups are dispatched round-robin over
-  // the XCDs (id % kXcds), so workgroup id w serves (sequence, kv head)
-  // group (w / kXcds / nq) * kXcds + w % kXcds and query tile
-  // (w / kXcds) % nq: all query tiles of one group run on one XCD and
-  // share its L2 copy of the group's K/V, and consecutive groups alternate
-  // XCDs.
+  // XCD-aware, longest-first order (chunks): workgroups are dispatched
+  // round-robin over the XCDs (id % kXcds) and, on each XCD, in id order as
+  // slots free up.  Workgroup id w serves group g = (w / kXcds / nq) *
+  // kXcds + w % kXcds -- kv head g % Hkv of the (g / Hkv)-th longest chunk
+  // sequence (the caller ranks them) -- and query tile nq - 1 - (w / kXcds)
+  // % nq: all query tiles of one group run on one XCD and share its L2 copy
+  // of the group's K/V, and each XCD starts with the longest tiles, which
+  // shortens the tail of the last wave of workgroups.
   int kvh, seq, q0, qlen, qt0, pos0, kb0, kend, mbeg = 0, split = 0;
   if constexpr (PFX) {
     const int item = unit;
@@ -517,10 +523,10 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
     const int grp = (slot / A.nq_tiles) * kXcds + wg % kXcds;
     if (grp >= A.num_groups) return;
     kvh = grp % num_kv_heads;
-    seq = A.seq_begin + grp / num_kv_heads;
+    seq = A.seq_begin + kvh_sel;
     q0 = A.cu[seq];
     qlen = A.cu[seq + 1] - q0;
-    qt0 = (slot % A.nq_tiles) * QT;
+    qt0 = (A.nq_tiles - 1 - slot % A.nq_tiles) * QT;
     if (qt0 >= qlen) return;
     const int ctxlen = min(A.ctx[seq], max_blocks * BS);
     pos0 = ctxlen - qlen;                                      // position of chunk row 0
@@ -819,11 +825,38 @@ __global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mf
   // make those reads wait for it.
   __shared__ __align__(16) uint16_t Ks0[L::TILE], Ks1[L::TILE], Vs0[L::TILE], Vs1[L::TILE];
   const int wg = (int)blockIdx.x;
-  if constexpr (PFX)
+  if constexpr (PFX) {
     chunk_mfma_body<T, D, G, BS, W, BPW, true>(a, wg / a.num_kv_heads, wg % a.num_kv_heads,
                                                (int)threadIdx.x, Ks0, Ks1, Vs0, Vs1);
-  else
-    chunk_mfma_body<T, D, G, BS, W, BPW, false>(a, wg, 0, (int)threadIdx.x, Ks0, Ks1, Vs0, Vs1);
+  } else {
+    // This workgroup's group rank r = g / Hkv (see chunk_mfma_body) names
+    // the r-th chunk sequence by descending context length (ties by index):
+    // the longest sequences' tiles are dispatched first.  Every workgroup
+    // ranks the sequences itself (kChunkRankMax of them at most; beyond
+    // that the order is the index order).
+    __shared__ int s_ctx[kChunkRankMax];
+    __shared__ int s_pick;
+    const int grp = (wg / kXcds / a.nq_tiles) * kXcds + wg % kXcds;
+    const int nseq = a.num_groups / a.num_kv_heads;
+    int pick = grp / a.num_kv_heads;
+    if (grp < a.num_groups && nseq > 1 && nseq <= kChunkRankMax) {
+      for (int t = threadIdx.x; t < nseq; t += blockDim.x) s_ctx[t] = a.ctx[a.seq_begin + t];
+      __syncthreads();
+      for (int t = threadIdx.x; t < nseq; t += blockDim.x) {
+        const int c = s_ctx[t];
+        int rank = 0;
+        for (int u = 0; u < nseq; ++u) {
+          const int cu = s_ctx[u];
+          rank += (cu > c || (cu == c && u < t)) ? 1 : 0;
+        }
+        if (rank == pick) s_pick = t;
+      }
+      __syncthreads();
+      pick = s_pick;
+    }
+    chunk_mfma_body<T, D, G, BS, W, BPW, false>(a, wg, pick, (int)threadIdx.x, Ks0, Ks1, Vs0,
+                                                Vs1);
+  }
 }
 
 template <typename T, int D, int G, int BS, bool NT, int NBUF>
