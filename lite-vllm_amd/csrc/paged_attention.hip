@@ -432,11 +432,11 @@ __device__ __forceinline__ i16x4_t lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)p);
 }
 
-// Arguments of the MFMA attention body (prefill chunks or shared-prefix
-// units).
 // Chunk sequences a chunk workgroup ranks by length (more: index order).
 constexpr int kChunkRankMax = 256;
 
+// Arguments of the MFMA attention body (prefill chunks or shared-prefix
+// units).
 template <typename T>
 struct ChunkArgs {
   const T* __restrict__ q; int64_t q_stride;
@@ -449,10 +449,10 @@ struct ChunkArgs {
 
 // PFX = false: prefill chunks (causal, normalised output rows); `unit` is
 // the workgroup id and `kvh_sel` the chunk sequence (index from seq_begin)
-// the caller's longest-first order gives it.  PFX = true: one shared-prefix unit -- `unit` is the
-// work item, `kvh_sel` the kv head: up to QT group members against one
-// 128-key split of the group's prefix (no causal mask; every prefix key
-// precedes every member's query), writing prefix partials.
+// the caller's longest-first order gives it.  PFX = true: one shared-prefix
+// unit -- `unit` is the work item, `kvh_sel` the kv head: up to QT group
+// members against one 128-key split of the group's prefix (no causal mask;
+// every prefix key precedes every member's query), writing prefix partials.
 // The body runs on one team of W wavefronts (`tid` = thread index in the
 // team) with its own four LDS tiles.  Every early exit before the last
 // barrier depends only on (unit, its item), never on the team or the lane,
@@ -572,13 +572,28 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
   }
   const int last_blk = (kend - 1) / BS;
   const int64_t blk_elems = (int64_t)BS * tok_stride;
+  // Physical ids of this wavefront's blocks (blocks wave + W j of each
+  // tile), 64 tiles at a time: lane l of bids[j] holds tile bid_tb + l.
+  // Loaded ahead so staging a tile never waits for a block-table read.
+  int bids[BPW];
+  int bid_tb = 0;
+  auto load_bids = [&](int tb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+      const int b = bt[min((kb0 + (tb + lane) * KT) / BS + wave + W * j, last_blk)];
+      bids[j] = (b < 0 || b >= num_cache_blocks) ? 0 : b;
+    }
+    bid_tb = tb;
+  };
+  load_bids(0);
   // Wavefront w stages blocks w, w + W, ... (BPW of them) of the tile.
   auto stage = [&](uint16_t* Kst, uint16_t* Vst, int k0) {
+    const int tile = (k0 - kb0) / KT;
+    if (tile - bid_tb >= 64) load_bids(tile);   // contexts beyond 64 tiles
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
       const int blk = wave + W * j;
-      int b = bt[min(k0 / BS + blk, last_blk)];
-      b = (b < 0 || b >= num_cache_blocks) ? 0 : b;
+      const int b = __builtin_amdgcn_readlane(bids[j], tile - bid_tb);
       const T* kp = kc + (int64_t)b * blk_elems;
       const T* vp = vc + (int64_t)b * blk_elems;
       uint16_t* kd = Kst + 16 * blk * D;
@@ -814,6 +829,35 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
 }
 
 
+// The chunk sequence a chunk workgroup of group g serves: group rank
+// r = g / Hkv names the r-th chunk sequence by descending context length
+// (ties by index), so the longest sequences' tiles are dispatched first.
+// Every workgroup ranks the sequences itself (kChunkRankMax of them at
+// most; beyond that the order is the index order).  All threads of the
+// workgroup call it (it may hold two barriers).
+template <typename T>
+__device__ __forceinline__ int chunk_rank_pick(const ChunkArgs<T>& a, int grp, int* s_ctx,
+                                               int* s_pick) {
+  const int nseq = a.num_groups / a.num_kv_heads;
+  int pick = grp / a.num_kv_heads;
+  if (grp < a.num_groups && nseq > 1 && nseq <= kChunkRankMax) {
+    for (int t = threadIdx.x; t < nseq; t += blockDim.x) s_ctx[t] = a.ctx[a.seq_begin + t];
+    __syncthreads();
+    for (int t = threadIdx.x; t < nseq; t += blockDim.x) {
+      const int c = s_ctx[t];
+      int rank = 0;
+      for (int u = 0; u < nseq; ++u) {
+        const int cu = s_ctx[u];
+        rank += (cu > c || (cu == c && u < t)) ? 1 : 0;
+      }
+      if (rank == pick) *s_pick = t;
+    }
+    __syncthreads();
+    pick = *s_pick;
+  }
+  return pick;
+}
+
 // Prefill chunks (PFX = false) or the shared-prefix pass as a launch of its
 // own (PFX = true: workgroup = (item, kv head)).
 template <typename T, int D, int G, int BS, int W, int BPW, bool PFX>
@@ -829,31 +873,10 @@ __global__ __launch_bounds__(64 * W, PFX ? 1 : 8 / (W * BPW)) void attn_chunk_mf
     chunk_mfma_body<T, D, G, BS, W, BPW, true>(a, wg / a.num_kv_heads, wg % a.num_kv_heads,
                                                (int)threadIdx.x, Ks0, Ks1, Vs0, Vs1);
   } else {
-    // This workgroup's group rank r = g / Hkv (see chunk_mfma_body) names
-    // the r-th chunk sequence by descending context length (ties by index):
-    // the longest sequences' tiles are dispatched first.  Every workgroup
-    // ranks the sequences itself (kChunkRankMax of them at most; beyond
-    // that the order is the index order).
     __shared__ int s_ctx[kChunkRankMax];
     __shared__ int s_pick;
     const int grp = (wg / kXcds / a.nq_tiles) * kXcds + wg % kXcds;
-    const int nseq = a.num_groups / a.num_kv_heads;
-    int pick = grp / a.num_kv_heads;
-    if (grp < a.num_groups && nseq > 1 && nseq <= kChunkRankMax) {
-      for (int t = threadIdx.x; t < nseq; t += blockDim.x) s_ctx[t] = a.ctx[a.seq_begin + t];
-      __syncthreads();
-      for (int t = threadIdx.x; t < nseq; t += blockDim.x) {
-        const int c = s_ctx[t];
-        int rank = 0;
-        for (int u = 0; u < nseq; ++u) {
-          const int cu = s_ctx[u];
-          rank += (cu > c || (cu == c && u < t)) ? 1 : 0;
-        }
-        if (rank == pick) s_pick = t;
-      }
-      __syncthreads();
-      pick = s_pick;
-    }
+    const int pick = chunk_rank_pick(a, grp, s_ctx, &s_pick);
     chunk_mfma_body<T, D, G, BS, W, BPW, false>(a, wg, pick, (int)threadIdx.x, Ks0, Ks1, Vs0,
                                                 Vs1);
   }
