@@ -572,9 +572,10 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
   }
   const int last_blk = (kend - 1) / BS;
   const int64_t blk_elems = (int64_t)BS * tok_stride;
-  // Physical ids of this wavefront's blocks (blocks wave + W j of each
-  // tile), 64 tiles at a time: lane l of bids[j] holds tile bid_tb + l.
-  // Loaded ahead so staging a tile never waits for a block-table read.
+  // Chunks: physical ids of this wavefront's blocks (blocks wave + W j of
+  // each tile), 64 tiles at a time: lane l of bids[j] holds tile bid_tb + l,
+  // loaded ahead so staging a tile never waits for a block-table read.  (A
+  // shared-prefix unit has at most two tiles and reads its ids directly.)
   int bids[BPW];
   int bid_tb = 0;
   auto load_bids = [&](int tb) __attribute__((always_inline)) {
@@ -585,15 +586,23 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
     }
     bid_tb = tb;
   };
-  load_bids(0);
+  if constexpr (!PFX) load_bids(0);
   // Wavefront w stages blocks w, w + W, ... (BPW of them) of the tile.
   auto stage = [&](uint16_t* Kst, uint16_t* Vst, int k0) {
     const int tile = (k0 - kb0) / KT;
-    if (tile - bid_tb >= 64) load_bids(tile);   // contexts beyond 64 tiles
+    if constexpr (!PFX) {
+      if (tile - bid_tb >= 64) load_bids(tile);   // contexts beyond 64 tiles
+    }
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
       const int blk = wave + W * j;
-      const int b = __builtin_amdgcn_readlane(bids[j], tile - bid_tb);
+      int b;
+      if constexpr (PFX) {
+        b = bt[min(k0 / BS + blk, last_blk)];
+        b = (b < 0 || b >= num_cache_blocks) ? 0 : b;
+      } else {
+        b = __builtin_amdgcn_readlane(bids[j], tile - bid_tb);
+      }
       const T* kp = kc + (int64_t)b * blk_elems;
       const T* vp = vc + (int64_t)b * blk_elems;
       uint16_t* kd = Kst + 16 * blk * D;
