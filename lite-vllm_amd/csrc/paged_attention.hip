@@ -898,7 +898,7 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
     const int32_t* __restrict__ block_tables, int max_blocks, const int32_t* __restrict__ ctx,
     int num_seqs, float scale_log2, T* __restrict__ out, int64_t out_stride,
     int32_t* __restrict__ ws_off, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
-    PrefixArgs pfx) {
+    PrefixArgs pfx, int sync_mask) {
   using S = HeadState<T, D, G, BS, NT>;
   constexpr int VEC = S::VEC;
   // LDS: s_off [num_seqs + 1], then (shared prefixes only) s_skip [num_seqs]
@@ -1090,9 +1090,18 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
     // NBUF register buffers rotate: NBUF - 1 blocks are in flight while one
     // is folded in.  Loads past the group end reload its last block (cache
     // hit) and their visits are masked no-ops.
+    //
+    // Every sync_mask + 1 blocks the workgroup's wavefronts (one per kv
+    // head, all walking the same blocks) meet at a plain barrier (no memory
+    // fence: loads stay in flight across it).  Left alone they drift apart
+    // by up to a quarter of the kernel (the CU's memory pipeline does not
+    // serve its eight wavefronts evenly) and the last one finishes alone;
+    // in step, all of them end together.  Every wavefront runs the same
+    // loop trip counts, so each reaches the same barriers.
     if constexpr (NBUF == 2) {
       st.load(kbase, vbase, phys(0), blk_stride, tok_stride, k0, v0);
       for (int i = 0; i < cnt; i += 2) {
+        if (sync_mask >= 0 && (i & sync_mask) == 0) __builtin_amdgcn_s_barrier();
         st.load(kbase, vbase, phys(i + 1), blk_stride, tok_stride, k1, v1);
         __builtin_amdgcn_sched_barrier(0);
         visit(k0, v0, i);
@@ -1105,6 +1114,7 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
       st.load(kbase, vbase, phys(1), blk_stride, tok_stride, k1, v1);
       st.load(kbase, vbase, phys(2), blk_stride, tok_stride, k2, v2);
       for (int i = 0; i < cnt; i += 4) {
+        if (sync_mask >= 0 && (i & sync_mask) == 0) __builtin_amdgcn_s_barrier();
         st.load(kbase, vbase, phys(i + 3), blk_stride, tok_stride, k3, v3);
         __builtin_amdgcn_sched_barrier(0);
         visit(k0, v0, i);
@@ -1299,6 +1309,7 @@ struct AttnPlan {
   int part_tokens;  // rows kernel
   int max_parts;    // rows kernel
   int num_wgs;      // persistent kernel
+  int sync_mask;    // persistent kernel: barrier every sync_mask + 1 blocks (-1: none)
   size_t off_bytes, ml_bytes, acc_bytes;  // off_bytes: flattened block offsets
   size_t bytes() const { return off_bytes + ml_bytes + acc_bytes; }
 };
@@ -1314,6 +1325,11 @@ static AttnPlan plan_decode(int num_decodes, int num_heads, int num_kv_heads, in
     // NBUF - 1 blocks (8 KiB each at the Qwen3 shape) in flight.
     p.nbuf = env_int("LV_ATTN_NBUF", 2) == 4 ? 4 : 2;
     p.num_wgs = env_int("LV_ATTN_PERSIST_WGS", device_cu_count() * (num_kv_heads == 1 ? 4 : 1));
+    // wavefront lockstep interval in blocks (LV_ATTN_SYNC=0: none)
+    int sync = env_is("LV_ATTN_SYNC", '0') ? 0 : env_int("LV_ATTN_SYNC", 8);
+    int pow2 = 2;
+    while (pow2 < sync && pow2 < 64) pow2 *= 2;
+    p.sync_mask = sync > 0 ? pow2 - 1 : -1;
     // block offsets [num_decodes + 1] and shared-prefix skips [num_decodes]
     p.off_bytes = align256(sizeof(int32_t) * (size_t)(2 * num_decodes + 1));
     p.ml_bytes = align256(sizeof(float) * 2 * (size_t)p.num_wgs * 2 * num_heads);
@@ -1378,7 +1394,7 @@ static void launch_persistent(const void* q, int64_t q_stride, const void* kc, c
   hipLaunchKernelGGL((attn_decode_persistent_kernel<T, D, G, BS, NT, NBUF>), dim3(p.num_wgs),
                      dim3(64 * num_kv_heads), lds, st, (const T*)q, q_stride, (const T*)kc,
                      (const T*)vc, num_kv_heads, num_cache_blocks, bt, max_blocks, ctx, num_seqs,
-                     scale_log2, (T*)out, out_stride, ws_off, ws_acc, ws_ml, pfx);
+                     scale_log2, (T*)out, out_stride, ws_off, ws_acc, ws_ml, pfx, p.sync_mask);
   hipLaunchKernelGGL((attn_persist_reduce_kernel<T, D>), dim3(num_seqs, num_kv_heads * G),
                      dim3(D), 0, st, (const int32_t*)ws_off, num_seqs, p.num_wgs,
                      num_kv_heads * G, (const float*)ws_acc, (const float*)ws_ml, (T*)out,
