@@ -417,13 +417,22 @@ __device__ void scan_block_counts(const int32_t* __restrict__ ctx,
 // sub-tiles of 64 keys.
 
 // LDS tile of K or V: 16 W key rows of D elements, unpadded; 16-byte chunk j
-// of row r holds the row's chunk j ^ (r % CPR).  The XOR swizzle lets 16 rows
-// read at one column land in 16 distinct bank quads.
+// of row r holds the row's chunk j ^ swz(r).  The XOR swizzle serves both
+// read patterns without bank conflicts: the K reads (eight consecutive rows
+// at one chunk per 128-byte LDS cycle) need swz distinct over rows 8i..8i+7,
+// and the V transpose reads (rows 4i..4i+3 at one 32-byte chunk pair per
+// 16-lane group) need swz / 2 distinct mod 4 over rows 4i..4i+3:
+// swz(r) = 2 (r % 4) + (r / 4) % 2 + 8 ((r / 8) % 2), restricted to
+// 0..CPR-1.  (Plain r % CPR fails the second: rows 0 and 1 share a chunk
+// pair's banks.)
 template <int D, int W> struct ChunkLds {
   static constexpr int CPR = D / 8;                 // 16-byte chunks per row
   static constexpr int TILE = 16 * W * D;           // elements per K or V tile
+  __device__ __forceinline__ static int swz(int row) {
+    return (((row & 3) << 1) | ((row >> 2) & 1) | (row & 8)) & (CPR - 1);
+  }
   __device__ __forceinline__ static int at(int row, int chunk) {
-    return row * D + 8 * (chunk ^ (row & (CPR - 1)));
+    return row * D + 8 * (chunk ^ swz(row));
   }
 };
 
@@ -562,12 +571,12 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
 
   // Staging: wavefront w loads block w of the tile (rows 16w..16w+15) with
   // LPW wave-wide loads; lane l of load u fills LDS slot l % CPR of row
-  // 16w + RPI u + l / CPR, i.e. the row's chunk (l % CPR) ^ (row % CPR).
+  // 16w + RPI u + l / CPR, i.e. the row's chunk (l % CPR) ^ swz(row).
   int64_t goff[LPW];
 #pragma unroll
   for (int u = 0; u < LPW; ++u) {
     const int r = RPI * u + lane / CPR;            // row inside the block
-    const int chunk = (lane % CPR) ^ (r & (CPR - 1));  // 16-row blocks keep row & 15
+    const int chunk = (lane % CPR) ^ L::swz(r);        // 16-row blocks keep row & 15
     goff[u] = (int64_t)r * tok_stride + (int64_t)kvh * D + 8 * chunk;
   }
   const int last_blk = (kend - 1) / BS;
@@ -630,12 +639,12 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
 
 
   // Per-lane LDS offsets of the MFMA operands.  Rows 32 kb + lr share
-  // lr's swizzle (row & (CPR - 1) == lr & (CPR - 1)), so the K offset of
-  // step st is kx[st] plus the constant 32 kb D; the V rows 16 t + vrow
-  // (+ 8) likewise share a swizzle across t.
+  // lr's swizzle (it depends on row % 16 only), so the K offset of step st
+  // is kx[st] plus the constant 32 kb D; the V rows 16 t + vrow (+ 8)
+  // likewise share a swizzle across t.
   int kx[QSTEPS];
   {
-    const int y = h ^ (lr & (CPR - 1));   // (2 st + h) ^ sw == 2 st ^ y
+    const int y = h ^ L::swz(lr);         // (2 st + h) ^ sw == 2 st ^ y
 #pragma unroll
     for (int st = 0; st < QSTEPS; ++st) kx[st] = lr * D + 8 * ((2 * st) ^ y);
   }
