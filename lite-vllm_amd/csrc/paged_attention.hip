@@ -417,19 +417,19 @@ __device__ void scan_block_counts(const int32_t* __restrict__ ctx,
 // sub-tiles of 64 keys.
 
 // LDS tile of K or V: 16 W key rows of D elements, unpadded; 16-byte chunk j
-// of row r holds the row's chunk j ^ swz(r).  The XOR swizzle serves both
-// read patterns without bank conflicts: the K reads (eight consecutive rows
-// at one chunk per 128-byte LDS cycle) need swz distinct over rows 8i..8i+7,
-// and the V transpose reads (rows 4i..4i+3 at one 32-byte chunk pair per
-// 16-lane group) need swz / 2 distinct mod 4 over rows 4i..4i+3:
-// swz(r) = 2 (r % 4) + (r / 4) % 2 + 8 ((r / 8) % 2), restricted to
-// 0..CPR-1.  (Plain r % CPR fails the second: rows 0 and 1 share a chunk
-// pair's banks.)
+// of row r holds the row's chunk j ^ swz(r % 16).  The XOR swizzle keeps
+// both read patterns free of bank conflicts on 64 banks of 4 bytes: the K
+// reads (16 consecutive rows at one chunk per LDS cycle) need swz to be a
+// permutation of 0..15, and the V transpose reads (32 lanes per cycle:
+// rows 4i..4i+3 at four consecutive chunks) need bits 2-3 of swz distinct
+// over rows 4i..4i+3 -- and bits 1-2 as well, for the 16-lane, 32-bank
+// grouping.  swz = 0 6 10 12 1 7 11 13 2 4 8 14 3 5 9 15 meets all three;
+// plain r % 16 makes rows 4i..4i+3 share banks.  (D = 64 takes swz % 8.)
 template <int D, int W> struct ChunkLds {
   static constexpr int CPR = D / 8;                 // 16-byte chunks per row
   static constexpr int TILE = 16 * W * D;           // elements per K or V tile
   __device__ __forceinline__ static int swz(int row) {
-    return (((row & 3) << 1) | ((row >> 2) & 1) | (row & 8)) & (CPR - 1);
+    return (int)((0xF953E842DB71CA60ull >> (4 * (row & 15))) & (CPR - 1));
   }
   __device__ __forceinline__ static int at(int row, int chunk) {
     return row * D + 8 * (chunk ^ swz(row));
