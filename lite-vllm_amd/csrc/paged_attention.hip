@@ -657,23 +657,28 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
     voff[b][1] = L::at(vrow + 8, dim >> 3) + (dim & 7);
   }
 
-  // S^T of one 64-key sub-tile (raw scores, two 32-key halves); K operands
-  // are read four steps ahead of their MFMAs.
+  // S^T of one 64-key sub-tile (raw scores, two 32-key halves): 16 MFMAs,
+  // step j = (half j / 8, k-step j % 8), with four K operand reads in
+  // flight.  The order is pinned (read j + 4 goes out right after MFMA j
+  // frees its buffer): left to itself the scheduler, at this register
+  // budget, gives all reads one buffer and waits out each read in turn.
   auto qk = [&](const uint16_t* kb_lds, f32x16_t* sv) {
+    auto kread = [&](int j) __attribute__((always_inline)) {
+      return *reinterpret_cast<const uint4*>(kb_lds + 32 * (j >> 3) * D + kx[j & 7]);
+    };
+    static_assert(QSTEPS == 8 || QSTEPS == 4, "head_dim 128 or 64");
+    constexpr int NJ = 2 * QSTEPS;
+    uint4 ka[4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const uint16_t* kbase = kb_lds + 32 * kb * D;
-      uint4 ka[4];
+    for (int j = 0; j < 4; ++j) ka[j] = kread((j / QSTEPS) * 8 + j % QSTEPS);
 #pragma unroll
-      for (int st = 0; st < 4; ++st) ka[st] = *reinterpret_cast<const uint4*>(kbase + kx[st]);
-      sv[kb] = M::run(__builtin_bit_cast(v8, ka[0]), qf[0], f32x16_t{});
-#pragma unroll
-      for (int st = 1; st < QSTEPS; ++st) {
-        if (st + 3 < QSTEPS)
-          ka[(st + 3) & 3] = *reinterpret_cast<const uint4*>(kbase + kx[st + 3]);
-        sv[kb] = M::run(__builtin_bit_cast(v8, ka[st & 3]), qf[st], sv[kb]);
-      }
+    for (int j = 0; j < NJ; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int kb = j / QSTEPS, st = j % QSTEPS;
+      sv[kb] = M::run(__builtin_bit_cast(v8, ka[j & 3]), qf[st], st ? sv[kb] : f32x16_t{});
+      if (j + 4 < NJ) ka[j & 3] = kread(((j + 4) / QSTEPS) * 8 + (j + 4) % QSTEPS);
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
   // Causal / range mask (MaskT = std::true_type on tiles that may need it;
   // those run in a loop of their own so the mask is never straight-line code
