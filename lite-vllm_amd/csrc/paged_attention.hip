@@ -1153,13 +1153,16 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
 // tokens.  Partials are merged in a fixed order: walked pieces in range
 // order, then prefix splits in key order.
 template <typename T, int D>
-__global__ __launch_bounds__(D) void attn_persist_reduce_kernel(
+__global__ __launch_bounds__(512) void attn_persist_reduce_kernel(
     const int32_t* __restrict__ ws_off, int num_seqs, int num_wgs, int num_heads,
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     T* __restrict__ out, int64_t out_stride, PrefixArgs pfx, int block_size) {
+  // workgroup = (sequence, 512 / D query heads); thread = (head, dim)
+  constexpr int HPW = 512 / D;
   const int sq = blockIdx.x;
-  const int hq = blockIdx.y;
-  const int d = threadIdx.x;
+  const int hq = blockIdx.y * HPW + (int)threadIdx.x / D;
+  const int d = (int)threadIdx.x % D;
+  if (hq >= num_heads) return;
   const int a = ws_off[sq], b = ws_off[sq + 1];
   const RangeSplit rs = make_range_split(ws_off[num_seqs], num_wgs);
   T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + d;
@@ -1409,10 +1412,12 @@ static void launch_persistent(const void* q, int64_t q_stride, const void* kc, c
                      dim3(64 * num_kv_heads), lds, st, (const T*)q, q_stride, (const T*)kc,
                      (const T*)vc, num_kv_heads, num_cache_blocks, bt, max_blocks, ctx, num_seqs,
                      scale_log2, (T*)out, out_stride, ws_off, ws_acc, ws_ml, pfx, p.sync_mask);
-  hipLaunchKernelGGL((attn_persist_reduce_kernel<T, D>), dim3(num_seqs, num_kv_heads * G),
-                     dim3(D), 0, st, (const int32_t*)ws_off, num_seqs, p.num_wgs,
-                     num_kv_heads * G, (const float*)ws_acc, (const float*)ws_ml, (T*)out,
-                     out_stride, pfx, BS);
+  constexpr int kHeadsPerReduceWg = 512 / D;
+  const int H = num_kv_heads * G;
+  hipLaunchKernelGGL((attn_persist_reduce_kernel<T, D>),
+                     dim3(num_seqs, (H + kHeadsPerReduceWg - 1) / kHeadsPerReduceWg), dim3(512),
+                     0, st, (const int32_t*)ws_off, num_seqs, p.num_wgs, H,
+                     (const float*)ws_acc, (const float*)ws_ml, (T*)out, out_stride, pfx, BS);
 }
 
 // Everything one launch needs besides the dtype / shape template arguments.

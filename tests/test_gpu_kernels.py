@@ -152,6 +152,30 @@ def test_decode_workspace_reuse_and_counter_reset(device):
         _check_attention(got, _oracle(batch), f"reuse seed={seed}")
 
 
+@pytest.mark.parametrize("heads", [(16, 8, 128), (8, 1, 64), (32, 4, 128)])
+def test_decode_lockstep_interval_bit_identical(device, heads, monkeypatch):
+    """The persistent kernel's wavefront lockstep barrier (LV_ATTN_SYNC,
+    default every 8 blocks) moves no data: outputs are bit-identical with it
+    off, at the default and at every 2 blocks; each run must also finish
+    (every wavefront of a workgroup reaches the same barriers)."""
+    H, Hkv, D = heads
+    _say(f"decode lockstep interval H={H} Hkv={Hkv} D={D}")
+    batch = workloads.paged_decode(seed=31, num_seqs=200, num_heads=H, num_kv_heads=Hkv,
+                                   head_dim=D, ctx_lo=1, ctx_hi=1500, scale_inputs=False,
+                                   ctx_head=[1, 2, 17, 33, 1024])
+    outs = {}
+    for sync in ("default", "0", "2"):
+        if sync == "default":
+            monkeypatch.delenv("LV_ATTN_SYNC", raising=False)
+        else:
+            monkeypatch.setenv("LV_ATTN_SYNC", sync)
+        outs[sync] = _run_attention(batch, device, use_cu=False).cpu()
+    monkeypatch.delenv("LV_ATTN_SYNC", raising=False)
+    _check_attention(outs["default"], _oracle(batch), f"lockstep {heads}")
+    assert torch.equal(outs["default"].view(torch.int16), outs["0"].view(torch.int16))
+    assert torch.equal(outs["default"].view(torch.int16), outs["2"].view(torch.int16))
+
+
 def test_decode_matches_reference_restatement(device):
     """The literal _decode_fast restatement (gather over max_s, mask, einsum)."""
     _say("decode vs literal _decode_fast restatement")
