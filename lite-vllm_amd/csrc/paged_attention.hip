@@ -1343,7 +1343,7 @@ static AttnPlan plan_decode(int num_decodes, int num_heads, int num_kv_heads, in
     p.nbuf = env_int("LV_ATTN_NBUF", 2) == 4 ? 4 : 2;
     p.num_wgs = env_int("LV_ATTN_PERSIST_WGS", device_cu_count() * (num_kv_heads == 1 ? 4 : 1));
     // wavefront lockstep interval in blocks (LV_ATTN_SYNC=0: none)
-    int sync = env_is("LV_ATTN_SYNC", '0') ? 0 : env_int("LV_ATTN_SYNC", 8);
+    int sync = env_is("LV_ATTN_SYNC", '0') ? 0 : env_int("LV_ATTN_SYNC", 4);
     int pow2 = 2;
     while (pow2 < sync && pow2 < 64) pow2 *= 2;
     p.sync_mask = sync > 0 ? pow2 - 1 : -1;

@@ -155,7 +155,7 @@ def test_decode_workspace_reuse_and_counter_reset(device):
 @pytest.mark.parametrize("heads", [(16, 8, 128), (8, 1, 64), (32, 4, 128)])
 def test_decode_lockstep_interval_bit_identical(device, heads, monkeypatch):
     """The persistent kernel's wavefront lockstep barrier (LV_ATTN_SYNC,
-    default every 8 blocks) moves no data: outputs are bit-identical with it
+    default every 4 blocks) moves no data: outputs are bit-identical with it
     off, at the default and at every 2 blocks; each run must also finish
     (every wavefront of a workgroup reaches the same barriers)."""
     H, Hkv, D = heads
