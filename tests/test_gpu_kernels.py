@@ -225,6 +225,21 @@ def test_chunk_lengths_and_offsets(device):
         _check_attention(got, _oracle(step.batch), f"chunk len={chunk_len} off={off}")
 
 
+def test_chunks_beyond_64_tiles(device):
+    """Chunk rows whose keys run past 64 tiles of 64 keys (contexts beyond
+    4096 tokens): the block ids each wavefront prefetches 64 tiles at a time
+    are refilled mid-row.  One pair of chunks straddles the 4096-key edge,
+    the other runs to ~12k keys (two refills)."""
+    for seed, off_lo, off_hi, L in ((41, 3990, 3990, 130), (42, 8000, 12000, 96)):
+        _say(f"chunks beyond 64 tiles off={off_lo}..{off_hi} len={L}")
+        step = workloads.mixed_step(seed=seed, num_decodes=4, dec_lo=1, dec_hi=6000,
+                                    num_chunks=2, chunk_len=L, off_lo=off_lo, off_hi=off_hi,
+                                    num_cache_slots=16 * 4096)
+        assert int(step.batch.context_lens.max()) > 64 * 64
+        got = _run_attention(step.batch, device, use_cu=True)
+        _check_attention(got, _oracle(step.batch), f"long chunks off={off_lo}")
+
+
 def test_mixed_config3_full(device):
     """The full config-3 step: 192 decodes + 15 chunks of 512 at offsets up
     to 3072, 200k-slot cache, N(0,1) values."""
