@@ -176,6 +176,30 @@ def test_decode_lockstep_interval_bit_identical(device, heads, monkeypatch):
     assert torch.equal(outs["default"].view(torch.int16), outs["2"].view(torch.int16))
 
 
+@pytest.mark.parametrize("knobs", [
+    {"LV_ATTN_NBUF": "4"}, {"LV_ATTN_NT": "0"}, {"LV_ATTN_PERSIST_WGS": "97"},
+    {"LV_ATTN_DECODE_KERNEL": "rows"},
+    {"LV_ATTN_DECODE_KERNEL": "rows", "LV_ATTN_PART_TOKENS": "128"},
+    {"LV_ATTN_CHUNK_KERNEL": "rows"}])
+def test_attention_tuning_knobs(device, knobs, monkeypatch):
+    """The per-call tuning knobs of lv_paged_attention (register buffers,
+    load type, persistent grid, the fallback row kernels and their partition
+    size) keep a mixed step within the attention bar; the two that change
+    only prefetch depth or load type leave it bit-identical."""
+    _say(f"attention knobs {knobs}")
+    step = workloads.mixed_step(seed=13, num_decodes=40, dec_lo=1, dec_hi=2500, num_chunks=3,
+                                chunk_len=90, off_hi=700, num_cache_slots=16 * 3000)
+    base = _run_attention(step.batch, device, use_cu=True).cpu()
+    for k, v in knobs.items():
+        monkeypatch.setenv(k, v)
+    got = _run_attention(step.batch, device, use_cu=True).cpu()
+    for k in knobs:
+        monkeypatch.delenv(k)
+    _check_attention(got, _oracle(step.batch), f"knobs {knobs}")
+    if set(knobs) <= {"LV_ATTN_NBUF", "LV_ATTN_NT"}:
+        assert torch.equal(got.view(torch.int16), base.view(torch.int16))
+
+
 def test_decode_matches_reference_restatement(device):
     """The literal _decode_fast restatement (gather over max_s, mask, einsum)."""
     _say("decode vs literal _decode_fast restatement")
