@@ -1612,33 +1612,27 @@ static int paged_attention_impl(const void* query_dev, int64_t q_stride_t,
                num_cache_blocks, block_tables_dev, max_blocks, nullptr, num_seqs,
                context_lens_dev, 0, 0, scale_log2, out_dev, out_stride_t, (hipStream_t)stream};
 
+  // Decode rows: plan and checks first, so a bad workspace or prefix plan
+  // fails before anything is launched.
+  AttnPlan pd{};
   if (num_decodes > 0) {
-    const AttnPlan p = plan_decode(num_decodes, num_heads, num_kv_heads, head_dim, block_size,
-                                   max_blocks);
-    if (p.bytes() > 0 && (workspace_dev == nullptr || workspace_bytes < p.bytes() ||
-                          (reinterpret_cast<uintptr_t>(workspace_dev) & 255) != 0)) {
+    pd = plan_decode(num_decodes, num_heads, num_kv_heads, head_dim, block_size, max_blocks);
+    if (pd.bytes() > 0 && (workspace_dev == nullptr || workspace_bytes < pd.bytes() ||
+                           (reinterpret_cast<uintptr_t>(workspace_dev) & 255) != 0)) {
       set_error("lv_paged_attention: workspace needs %zu bytes (256-B aligned), got %zu",
-                p.bytes(), workspace_bytes);
+                pd.bytes(), workspace_bytes);
       return LV_ERR_WORKSPACE;
     }
-    // Decode rows come first, so row i is sequence i: no cu_seqlens lookup.
-    a.cu = nullptr;
-    a.num_seqs = num_decodes;
-    a.row_begin = 0;
-    a.n_rows = num_decodes;
-    if (pfx) {
-      if (!p.persistent || dtype == LV_F32 || (head_dim != 64 && head_dim != 128) ||
-          block_size != 16 || !(G == 1 || G == 2 || G == 4 || G == 8) ||
-          num_decodes > kPrefixMaxRows) {
-        set_error("lv_paged_attention_prefix: no shared-prefix path for this shape");
-        return LV_ERR_UNSUPPORTED;
-      }
-      a.pfx = *pfx;
+    if (pfx && (!pd.persistent || dtype == LV_F32 || (head_dim != 64 && head_dim != 128) ||
+                block_size != 16 || !(G == 1 || G == 2 || G == 4 || G == 8) ||
+                num_decodes > kPrefixMaxRows)) {
+      set_error("lv_paged_attention_prefix: no shared-prefix path for this shape");
+      return LV_ERR_UNSUPPORTED;
     }
-    const int rc = dispatch(dtype, head_dim, G, block_size, a, p, (char*)workspace_dev);
-    a.pfx = PrefixArgs{};
-    if (rc != LV_OK) return rc;
   }
+  // Chunk rows go first: the K/V rows this step just wrote are still in the
+  // last-level cache for them; the decode rows' walk reads far more than it
+  // holds either way.
   if (num_decodes < num_seqs && dtype != LV_F32 && (head_dim == 64 || head_dim == 128) &&
       block_size == 16 && (G == 1 || G == 2 || G == 4 || G == 8) &&
       !env_is("LV_ATTN_CHUNK_KERNEL", 'r')) {
@@ -1660,6 +1654,18 @@ static int paged_attention_impl(const void* query_dev, int64_t q_stride_t,
     a.row_begin = num_decodes;
     a.n_rows = (int)(num_tokens - num_decodes);
     const int rc = dispatch(dtype, head_dim, G, block_size, a, p, nullptr);
+    if (rc != LV_OK) return rc;
+  }
+  if (num_decodes > 0) {
+    // Decode rows come first in the batch, so row i is sequence i: no
+    // cu_seqlens lookup.
+    a.cu = nullptr;
+    a.num_seqs = num_decodes;
+    a.row_begin = 0;
+    a.n_rows = num_decodes;
+    if (pfx) a.pfx = *pfx;
+    const int rc = dispatch(dtype, head_dim, G, block_size, a, pd, (char*)workspace_dev);
+    a.pfx = PrefixArgs{};
     if (rc != LV_OK) return rc;
   }
   return check_launch("lv_paged_attention");
