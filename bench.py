@@ -249,6 +249,15 @@ def bench_mixed(args):
 
     total_ms, per = _time_gpu(step, args.steps, args.warmup)
     kern_ms = statistics.mean(per)
+    result = {
+        "value": round(T / (kern_ms * 1e-3), 1), "unit": "packed tokens/s",
+        "ms_per_step": round(total_ms / args.steps, 4),
+        "config": {"workload": "config3 mixed step: 192 decodes ctx U[256,4096] + 15 chunks x 512 "
+                               "at offset U[0,3072], 200k-slot cache, bf16",
+                   "num_tokens": T},
+    }
+    if args.no_secondary:      # (keeps a kernel trace of this run to the step itself)
+        return result
 
     # The chunk rows alone (decode rows come first in the batch), same cache,
     # tables and lengths: the MFMA kernel's rate, HIP events on the launch
@@ -278,22 +287,16 @@ def bench_mixed(args):
     _, per_c = _time_gpu(chunk_call, args.steps, args.warmup)
     chunk_ms = statistics.mean(per_c)
     tflops = flops / (chunk_ms * 1e-3) / 1e12
-    return {
-        "value": round(T / (kern_ms * 1e-3), 1), "unit": "packed tokens/s",
-        "ms_per_step": round(total_ms / args.steps, 4),
-        "config": {"workload": "config3 mixed step: 192 decodes ctx U[256,4096] + 15 chunks x 512 "
-                               "at offset U[0,3072], 200k-slot cache, bf16",
-                   "num_tokens": T},
-        "chunk_roofline": {
-            "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "algorithmic_flops": flops, "avg_launch_us": round(chunk_ms * 1e3, 2),
-            "kernel": "attn_chunk_mfma_kernel (lv_paged_attention on the chunk rows alone)",
-            "note": "repeated chunk-only calls keep the chunks' K/V (~140 MB) in the MALL; "
-                    "inside the mixed step the decode kernel runs first and the chunk "
-                    "kernel reads a few percent slower (rocprof trace of this workload)",
-        },
+    result["chunk_roofline"] = {
+        "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        "algorithmic_flops": flops, "avg_launch_us": round(chunk_ms * 1e3, 2),
+        "kernel": "attn_chunk_mfma_kernel (lv_paged_attention on the chunk rows alone)",
+        "note": "repeated chunk-only calls keep the chunks' K/V (~140 MB) in the MALL, so "
+                "they read faster than the chunk kernel inside the step (rocprof trace of "
+                "this workload with --no-secondary)",
     }
+    return result
 
 
 def bench_e2e(args):
@@ -570,7 +573,8 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true",
                     help="e2e: no HIP graphs for decode steps")
     ap.add_argument("--no-secondary", action="store_true",
-                    help="e2e: skip the config-2 decode-attention microbench")
+                    help="e2e: skip the config-2 decode-attention microbench; mixed: skip "
+                         "the chunk-rows-alone timing")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = 1 if args.workload == "e2e" else 50
