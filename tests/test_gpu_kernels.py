@@ -152,6 +152,18 @@ def test_decode_workspace_reuse_and_counter_reset(device):
         _check_attention(got, _oracle(batch), f"reuse seed={seed}")
 
 
+def test_decode_long_contexts(device):
+    """Rows of 16k-32k tokens among short ones: each workgroup walks many
+    64-block groups, and a long row spreads over dozens of workgroup ranges,
+    so the reduce takes its general (many-piece) merge path."""
+    _say("decode long contexts")
+    batch = workloads.paged_decode(seed=17, num_seqs=40, ctx_lo=1, ctx_hi=600,
+                                   scale_inputs=False, tail_fill=float("nan"),
+                                   ctx_head=[32768, 20000, 16385, 31999, 1])
+    got = _run_attention(batch, device, use_cu=False)
+    _check_attention(got, _oracle(batch), "long contexts")
+
+
 @pytest.mark.parametrize("heads", [(16, 8, 128), (8, 1, 64), (32, 4, 128)])
 def test_decode_lockstep_interval_bit_identical(device, heads, monkeypatch):
     """The persistent kernel's wavefront lockstep barrier (LV_ATTN_SYNC,
