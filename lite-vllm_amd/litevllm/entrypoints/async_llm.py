@@ -14,7 +14,9 @@ loop with ``call_soon_threadsafe``; every request has its own
 ``asyncio.Queue`` of deltas closed by an end marker.  If a step raises,
 the error is delivered to every open stream (each ``stream`` raises it)
 and later requests are refused.  A consumer that stops reading a stream
-early aborts its request, which frees its KV blocks.
+early aborts its request, which frees its KV blocks.  ``shutdown`` ends
+every stream still open (each raises ``RuntimeError``), including requests
+posted after it, and later requests are refused.
 """
 
 from __future__ import annotations
@@ -48,6 +50,7 @@ class AsyncLLM:
         self._wake = threading.Condition()
         self._thread: Optional[threading.Thread] = None
         self._error: Optional[BaseException] = None
+        self._closed = False                       # shutdown() was called
 
     # -- lifecycle ---------------------------------------------------------
     async def initialize(self) -> None:
@@ -62,7 +65,9 @@ class AsyncLLM:
         self._thread.start()
 
     async def shutdown(self) -> None:
-        """Stop the engine thread (unfinished requests are dropped)."""
+        """Stop the engine thread.  Unfinished requests are dropped: their
+        streams raise ``RuntimeError`` instead of waiting forever."""
+        self._closed = True
         if self._thread is not None:
             self._post("stop", None)
             await self._loop.run_in_executor(None, self._thread.join)
@@ -72,6 +77,8 @@ class AsyncLLM:
     async def add_request(self, prompt: Optional[str], sampling_params: SamplingParams,
                           request_id: Optional[str] = None,
                           prompt_token_ids: Optional[list[int]] = None) -> str:
+        if self._closed:
+            raise RuntimeError("AsyncLLM is shut down")
         if self._thread is None:
             raise RuntimeError("AsyncLLM is not initialized (await initialize() first)")
         if self._error is not None:
@@ -146,6 +153,10 @@ class AsyncLLM:
                 self._inbox.clear()
             for command, payload in commands:
                 if command == "stop":
+                    # every stream still open ends now, also those whose
+                    # "add" came after the stop (never applied: the engine
+                    # is not stepped again)
+                    self._to_loop(self._fail_all, RuntimeError("AsyncLLM shut down"))
                     return
                 if command == "add":
                     rid, prompt, params, ids = payload

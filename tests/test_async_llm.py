@@ -165,3 +165,29 @@ def test_failed_step_reaches_every_stream_and_refuses_new_requests(fake):
         with pytest.raises(RuntimeError, match="engine thread failed"):
             await llm.add_request(None, SamplingParams(), prompt_token_ids=[1])
     _run(main())
+
+
+def test_shutdown_ends_open_streams_and_refuses_new_requests(fake):
+    async def main():
+        llm = mod.AsyncLLM(_cfg())
+        await llm.initialize()
+        got = []
+
+        async def collect(rid, n):
+            async for d in llm.stream(None, SamplingParams(max_tokens=n), request_id=rid,
+                                      prompt_token_ids=[1]):
+                got.append((rid, d))
+        long = asyncio.ensure_future(collect("long", 10**9))
+        while len(got) < 2:
+            await asyncio.sleep(0.001)
+        # posted right before the stop: applied or not, its stream must end
+        late = asyncio.ensure_future(collect("late", 10**9))
+        await asyncio.sleep(0)
+        await llm.shutdown()
+        for task in (long, late):
+            with pytest.raises(RuntimeError) as e:
+                await task
+            assert "shut down" in str(e.value.__cause__)
+        with pytest.raises(RuntimeError, match="shut down"):
+            await llm.add_request(None, SamplingParams(), prompt_token_ids=[1])
+    _run(main())
