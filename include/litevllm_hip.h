@@ -43,7 +43,8 @@ typedef enum lv_status {
   LV_ERR_INVALID = -1,     /* bad shape, stride, alignment or pointer */
   LV_ERR_HIP = -2,         /* a HIP runtime call or launch failed */
   LV_ERR_WORKSPACE = -3,   /* workspace missing or too small */
-  LV_ERR_UNSUPPORTED = -4  /* valid request this build has no kernel for */
+  LV_ERR_UNSUPPORTED = -4, /* valid request this build has no kernel for */
+  LV_ERR_DEVICE_INDEX = -5 /* lv_device_errors: a kernel met an out-of-range index */
 } lv_status;
 
 /* Thread-local description of the last error on this thread ("" if none). */
@@ -51,7 +52,32 @@ const char* lv_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int lv_abi_version(void);
-#define LV_ABI_VERSION 6
+#define LV_ABI_VERSION 7
+
+/* Out-of-range indices met by the kernels on the current device.
+ *
+ * The reference's torch indexing raises on an index outside its tensor
+ * (litevllm/layers/attention.py:80-84 slot_mapping into the caches,
+ * 111-119 block_table into the caches).  The kernels here never access
+ * memory outside a buffer: they clamp such an index (a block id outside
+ * [0, num_cache_blocks) reads block 0; a slot >= num_blocks * block_size is
+ * not written) and raise a bit in a device-side error word:
+ *   LV_DEVERR_BLOCK_ID  a block-table entry outside [0, num_cache_blocks)
+ *                       (lv_paged_attention, lv_paged_attention_prefix)
+ *   LV_DEVERR_SLOT      a slot_mapping entry >= num_blocks * block_size
+ *                       (lv_kv_scatter, lv_qk_norm_rope_cache)
+ * Negative slots are padding (skipped, no bit).
+ * lv_device_errors waits for the current device (hipDeviceSynchronize), so
+ * every kernel enqueued before the call has reported, then stores the bits
+ * raised since the last clear in *flags_out (may be NULL) and, if clear is
+ * nonzero, resets them.  Returns LV_OK when no bit is set,
+ * LV_ERR_DEVICE_INDEX (with lv_last_error naming the bits) when one is, or
+ * LV_ERR_HIP.  The word is per device and per process, shared by every
+ * stream: a clear races with kernels another thread enqueues meanwhile.
+ */
+#define LV_DEVERR_BLOCK_ID 1u
+#define LV_DEVERR_SLOT 2u
+int lv_device_errors(uint32_t* flags_out, int32_t clear);
 
 /* ------------------------------------------------------------------------
  * (1) Ragged-batch packing.
@@ -120,7 +146,7 @@ int lv_pack_inputs(const lv_seq_desc* descs_dev, int32_t num_seqs,
  * (elements), heads contiguous.  Caches: contiguous
  * [num_blocks, block_size, num_kv_heads, head_dim].  Slots < 0 are skipped
  * (padding); slots >= num_blocks*block_size are skipped so no write leaves
- * the cache.  Duplicate slots in one call: last writer undefined (torch's
+ * the cache, and raise LV_DEVERR_SLOT (see lv_device_errors).  Duplicate slots in one call: last writer undefined (torch's
  * index_put is undefined there too).
  */
 int lv_kv_scatter(const void* key_dev, int64_t key_stride_t,
@@ -153,13 +179,18 @@ int lv_kv_scatter(const void* key_dev, int64_t key_stride_t,
  * with out_stride_t.  Caches as in lv_kv_scatter.  block_tables:
  * [num_seqs, max_blocks] int32.
  * num_cache_blocks bounds every block id read from block_tables (an id
- * outside [0, num_cache_blocks) reads block 0 instead of faulting); context
- * lengths are clamped to max_blocks * block_size.
+ * outside [0, num_cache_blocks) reads block 0 instead of faulting and raises
+ * LV_DEVERR_BLOCK_ID, see lv_device_errors); context lengths are clamped to
+ * max_blocks * block_size.
  * workspace: at least lv_paged_attention_workspace_size(...) bytes, 256-B
  * aligned; contents need not be initialised.  Calls that overlap on one
  * workspace race (use one workspace per stream).
  * Supported: head_dim 64 or 128, block_size 16, num_heads / num_kv_heads in
- * {1, 2, 4, 8}; anything else returns LV_ERR_UNSUPPORTED.
+ * {1, 2, 4, 8}; anything else returns LV_ERR_UNSUPPORTED.  Decode rows run on
+ * the persistent kernel (num_kv_heads <= 8, num_decodes <= 15000), which
+ * indexes its flattened block list in 32 bits: there num_decodes *
+ * max_blocks above 2^31 - 2^16 returns LV_ERR_INVALID (the row kernel,
+ * LV_ATTN_DECODE_KERNEL=rows, has no such limit).
  */
 size_t lv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_decodes,
                                          int64_t num_tokens, int32_t num_heads,
@@ -271,7 +302,9 @@ int lv_sample(const void* logits_dev, int64_t num_rows, int64_t vocab_size,
  * under HIP graph capture, tight serving loops, harnesses that forbid it).
  * Arguments, results and errors are those of lv_sample.  Its scratch is a
  * fixed 4 MiB array in the library's device code, one copy per GPU, looked
- * up on the first call on each device; calls needing more than
+ * up (hipGetSymbolAddress) on the first call on each device -- make that
+ * first call outside any stream capture (a warm-up call), so the lookup is
+ * not made while a graph is being recorded; calls needing more than
  * lv_sample_workspace_size(num_rows, vocab_size) <= 4 MiB (e.g. above 1765
  * rows at vocab 151936) are rejected with LV_ERR_WORKSPACE.  Every call on a
  * GPU uses that GPU's one copy: calls that overlap on one GPU (two streams,
@@ -316,7 +349,8 @@ int lv_add_rms_norm(const void* x_dev, int64_t x_stride_t, void* residual_dev,
  *   key_cache  row slot_mapping[t]  = rope(norm_k(k[t]), positions[t])
  *   value_cache row slot_mapping[t] = v[t]
  * Tokens with slot < 0 (padding) or slot >= num_blocks*block_size write no
- * cache row; a position outside [0, max_position) yields NaN rows.
+ * cache row (the latter raise LV_DEVERR_SLOT, see lv_device_errors); a
+ * position outside [0, max_position) yields NaN rows.
  * head_dim in {64, 128, 256}. */
 int lv_qk_norm_rope_cache(const void* qkv_dev, int64_t qkv_stride_t,
                           const void* q_norm_weight_dev, const void* k_norm_weight_dev,

@@ -114,8 +114,12 @@ __global__ __launch_bounds__(kFusedThreads) void qk_norm_rope_cache_kernel(
   const int64_t pos = positions[t];
   const int64_t slot = slots[t];
 
+  // a slot past the cache writes nothing and is reported (by the value
+  // head's first lane); slot < 0 is padding
+  const bool slot_ok = slot >= 0 && slot < num_slots;
   if (hs >= num_heads + num_kv_heads) {  // value head: plain copy into the cache
-    if (slot < 0 || slot >= num_slots) return;
+    if (slot >= num_slots && lane_in_group == 0) report_device_error(LV_DEVERR_SLOT);
+    if (!slot_ok) return;
     T* dst = value_cache + slot * ((int64_t)num_kv_heads * D) +
              (int64_t)(hs - num_heads - num_kv_heads) * D;
 #pragma unroll
@@ -128,7 +132,7 @@ __global__ __launch_bounds__(kFusedThreads) void qk_norm_rope_cache_kernel(
   }
 
   const bool is_q = hs < num_heads;
-  if (!is_q && (slot < 0 || slot >= num_slots)) return;
+  if (!is_q && !slot_ok) return;
   const T* nw = is_q ? q_norm_w : k_norm_w;
   float x1[PPL], x2[PPL], w1[PPL], w2[PPL];
 #pragma unroll
@@ -282,6 +286,8 @@ int launch_silu_mul(const void* in, int64_t is, void* out, int64_t os, int64_t n
 inline bool rows_aligned(const void* p, int64_t stride_elems, size_t esize) {
   return aligned16(p) && ((stride_elems * (int64_t)esize) & 15) == 0;
 }
+
+LV_ERROR_WORD_READER(read_errors_fused)
 
 }  // namespace lv
 

@@ -22,7 +22,11 @@ __global__ __launch_bounds__(kScatterThreads) void kv_scatter_kernel(
   const int64_t t = (int64_t)blockIdx.x * (kScatterThreads / 64) + wave;
   if (t >= num_tokens) return;
   const int64_t slot = slots[t];
-  if (slot < 0 || slot >= num_slots) return;
+  if (slot < 0) return;                      // padding
+  if (slot >= num_slots) {                   // outside the cache: not written, reported
+    if (lane == 0) report_device_error(LV_DEVERR_SLOT);
+    return;
+  }
   const Chunk* ks = reinterpret_cast<const Chunk*>(key + t * key_stride_bytes);
   const Chunk* vs = reinterpret_cast<const Chunk*>(value + t * value_stride_bytes);
   Chunk* kd = reinterpret_cast<Chunk*>(key_cache) + slot * row_chunks;
@@ -34,6 +38,8 @@ __global__ __launch_bounds__(kScatterThreads) void kv_scatter_kernel(
     vd[c] = vv;
   }
 }
+
+LV_ERROR_WORD_READER(read_errors_scatter)
 
 }  // namespace lv
 

@@ -185,4 +185,40 @@ __device__ __forceinline__ float group_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---------------------------------------------------------------------------
+// Device-side report of out-of-range indices.  A kernel that meets one
+// clamps it (no access leaves its buffer) and raises a bit (LV_DEVERR_*) in
+// the error word of its translation unit.  Device code is not linked across
+// units, so every unit has a word of its own per device; the unit's reader
+// (defined with LV_ERROR_WORD_READER) copies it out and lv_device_errors()
+// ORs the readers' results.
+// ---------------------------------------------------------------------------
+namespace {
+__device__ uint32_t tu_error_word = 0;
+}
+__device__ __forceinline__ void report_device_error(uint32_t bit) {
+  __hip_atomic_fetch_or(&tu_error_word, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Readers of the units that report (the caller has synchronised the device).
+int read_errors_scatter(uint32_t* bits, bool clear);
+int read_errors_attention(uint32_t* bits, bool clear);
+int read_errors_fused(uint32_t* bits, bool clear);
+
+#define LV_ERROR_WORD_READER(NAME)                                                        \
+  int NAME(uint32_t* bits, bool clear) {                                                   \
+    hipError_t e = hipMemcpyFromSymbol(bits, HIP_SYMBOL(tu_error_word), sizeof(uint32_t), 0, \
+                                       hipMemcpyDeviceToHost);                             \
+    if (e == hipSuccess && clear) {                                                        \
+      const uint32_t zero = 0;                                                             \
+      e = hipMemcpyToSymbol(HIP_SYMBOL(tu_error_word), &zero, sizeof(uint32_t), 0,         \
+                            hipMemcpyHostToDevice);                                        \
+    }                                                                                      \
+    if (e != hipSuccess) {                                                                 \
+      set_error(#NAME ": %s", hipGetErrorString(e));                                       \
+      return LV_ERR_HIP;                                                                   \
+    }                                                                                      \
+    return LV_OK;                                                                          \
+  }
+
 }  // namespace lv

@@ -180,8 +180,13 @@ struct HeadState {
     for (int base = 0; base < n; base += 64) {
       const int cnt = min(64, n - base);
       int id = 0;
-      if (lane < cnt) id = bt[first + stride * (base + lane)];
-      if (id < 0 || id >= num_cache_blocks) id = 0;
+      if (lane < cnt) {
+        id = bt[first + stride * (base + lane)];
+        if (id < 0 || id >= num_cache_blocks) {   // clamped and reported
+          report_device_error(LV_DEVERR_BLOCK_ID);
+          id = 0;
+        }
+      }
       auto phys = [&](int i) { return __builtin_amdgcn_readlane(id, min(i, cnt - 1)); };
       load(kbase, vbase, phys(0), blk_stride, tok_stride, k0, v0);
       for (int i = 0; i < cnt; i += 2) {
@@ -591,7 +596,9 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
       const int b = bt[min((kb0 + (tb + lane) * KT) / BS + wave + W * j, last_blk)];
-      bids[j] = (b < 0 || b >= num_cache_blocks) ? 0 : b;
+      const bool bad = b < 0 || b >= num_cache_blocks;   // clamped and reported
+      if (bad) report_device_error(LV_DEVERR_BLOCK_ID);
+      bids[j] = bad ? 0 : b;
     }
     bid_tb = tb;
   };
@@ -608,7 +615,10 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
       int b;
       if constexpr (PFX) {
         b = bt[min(k0 / BS + blk, last_blk)];
-        b = (b < 0 || b >= num_cache_blocks) ? 0 : b;
+        if (b < 0 || b >= num_cache_blocks) {   // clamped and reported
+          report_device_error(LV_DEVERR_BLOCK_ID);
+          b = 0;
+        }
       } else {
         b = __builtin_amdgcn_readlane(bids[j], tile - bid_tb);
       }
@@ -1083,8 +1093,11 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
       lseq = lo;
       lblk = j - s_off[lo] + (has_pfx ? s_skip[lo] : 0);   // block index in the table
       id = block_tables[(int64_t)lo * max_blocks + lblk];
+      if (id < 0 || id >= num_cache_blocks) {   // clamped and reported
+        report_device_error(LV_DEVERR_BLOCK_ID);
+        id = 0;
+      }
     }
-    if (id < 0 || id >= num_cache_blocks) id = 0;
     auto phys = [&](int i) { return __builtin_amdgcn_readlane(id, min(i, cnt - 1)); };
     // Start (or continue) the sequence of entry i, then fold its block in;
     // i >= cnt is a fully masked no-op so process() always runs.
@@ -1505,25 +1518,11 @@ static void launch_chunk_kernel_w(const LaunchArgs& a, const int32_t* cu, int se
                      dim3(64 * W), 0, a.st, ca);
 }
 
-// Chunk workgroup shape (LV_ATTN_CHUNK_CFG): 1 = 4 wavefronts x 64-key tiles
-// (two workgroups per CU), 2 = 8 wavefronts x 128-key tiles, 3 = 4
-// wavefronts x 128-key tiles in two pipelined halves (one workgroup per CU).
-static int chunk_cfg() {
-  static const int c = [] {
-    const int v = env_int("LV_ATTN_CHUNK_CFG", 1);
-    return (v >= 1 && v <= 3) ? v : 1;
-  }();
-  return c;
-}
-
+// Chunk workgroups: 4 wavefronts, 64-key tiles, two workgroups per CU.
 template <typename T, int D, int G>
 static void launch_chunk_kernel(const LaunchArgs& a, const int32_t* cu, int seq_begin, int n_seqs,
                                 int max_query_len) {
-  switch (chunk_cfg()) {
-    case 2: launch_chunk_kernel_w<T, D, G, 8, 1>(a, cu, seq_begin, n_seqs, max_query_len); break;
-    case 3: launch_chunk_kernel_w<T, D, G, 4, 2>(a, cu, seq_begin, n_seqs, max_query_len); break;
-    default: launch_chunk_kernel_w<T, D, G, 4, 1>(a, cu, seq_begin, n_seqs, max_query_len); break;
-  }
+  launch_chunk_kernel_w<T, D, G, 4, 1>(a, cu, seq_begin, n_seqs, max_query_len);
 }
 
 template <typename T, int D>
@@ -1548,6 +1547,8 @@ static int launch_chunks(lv_dtype dt, int D, int G, const LaunchArgs& a, const i
   return D == 128 ? launch_chunks_g<f16, 128>(G, a, cu, seq_begin, n_seqs, max_query_len)
                   : launch_chunks_g<f16, 64>(G, a, cu, seq_begin, n_seqs, max_query_len);
 }
+
+LV_ERROR_WORD_READER(read_errors_attention)
 
 }  // namespace lv
 
@@ -1603,8 +1604,6 @@ static int paged_attention_impl(const void* query_dev, int64_t q_stride_t,
              "lv_paged_attention: token strides smaller than num_heads*head_dim");
   LV_REQUIRE((int64_t)max_blocks * block_size <= (1ll << 24),
              "lv_paged_attention: max_blocks * block_size above 2^24 tokens");
-  LV_REQUIRE((int64_t)num_decodes * max_blocks <= (1ll << 31) - (1ll << 16),
-             "lv_paged_attention: num_decodes * max_blocks above 2^31 - 2^16");
 
   const int G = num_heads / num_kv_heads;
   const float scale_log2 = scale * 0x1.715476p+0f;
@@ -1617,6 +1616,10 @@ static int paged_attention_impl(const void* query_dev, int64_t q_stride_t,
   AttnPlan pd{};
   if (num_decodes > 0) {
     pd = plan_decode(num_decodes, num_heads, num_kv_heads, head_dim, block_size, max_blocks);
+    // the persistent kernel's flattened block list is indexed in 32 bits
+    LV_REQUIRE(!pd.persistent || (int64_t)num_decodes * max_blocks <= (1ll << 31) - (1ll << 16),
+               "lv_paged_attention: num_decodes * max_blocks above 2^31 - 2^16 (persistent "
+               "decode kernel; LV_ATTN_DECODE_KERNEL=rows has no such limit)");
     if (pd.bytes() > 0 && (workspace_dev == nullptr || workspace_bytes < pd.bytes() ||
                            (reinterpret_cast<uintptr_t>(workspace_dev) & 255) != 0)) {
       set_error("lv_paged_attention: workspace needs %zu bytes (256-B aligned), got %zu",

@@ -18,7 +18,9 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 LV_F32, LV_F16, LV_BF16 = 0, 1, 2
 LV_ACT_NONE, LV_ACT_SILU_MUL = 0, 1
-ABI_VERSION = 6
+ABI_VERSION = 7
+LV_ERR_DEVICE_INDEX = -5
+LV_DEVERR_BLOCK_ID, LV_DEVERR_SLOT = 1, 2
 
 # Every symbol the header declares, with (restype, argtypes).
 _c_i32, _c_i64, _c_f32, _c_p, _c_sz = (
@@ -27,6 +29,7 @@ _c_i32, _c_i64, _c_f32, _c_p, _c_sz = (
 SIGNATURES: dict[str, tuple] = {
     "lv_last_error": (ctypes.c_char_p, []),
     "lv_abi_version": (ctypes.c_int, []),
+    "lv_device_errors": (ctypes.c_int, [ctypes.POINTER(ctypes.c_uint32), _c_i32]),
     "lv_pack_inputs": (ctypes.c_int, [
         _c_p, _c_i32,            # descs, num_seqs
         _c_p, _c_i64,            # block_ids, num_block_ids

@@ -22,12 +22,14 @@ decode, as in the reference.
 
 from __future__ import annotations
 
+import os
 import uuid
 from dataclasses import dataclass
 from typing import Optional
 
 import torch
 
+from .. import ops
 from ..cache.block_manager import BlockManager
 from ..cache.prefix_cache import PrefixCache
 from ..config import EngineConfig, SamplingParams
@@ -61,6 +63,9 @@ class LLMEngine:
         self.stream_text = False   # AsyncLLM turns this on to get per-step deltas
         self._rng: Optional[torch.Generator] = None
         self._inflight: Optional[_InFlightStep] = None
+        # LITEVLLM_CHECK_INDICES=1: check the kernels' index report every step
+        # (one device synchronisation per step; otherwise once per generate)
+        self._check_every_step = os.environ.get("LITEVLLM_CHECK_INDICES", "0") == "1"
 
     def initialize(self) -> None:
         self.config.resolve()
@@ -124,7 +129,16 @@ class LLMEngine:
             for out in self.step():
                 if out.finished:
                     finished.append(out)
+        self.check_device_errors()
         return finished
+
+    def check_device_errors(self) -> None:
+        """Raise if a kernel met an out-of-range block id or slot since the
+        last check (the kernels clamp them; the reference's indexing would
+        have raised).  One device synchronisation."""
+        dev = torch.device(self.config.device) if self.model_runner is not None else None
+        if dev is not None and dev.type == "cuda":
+            ops.check_device_errors(dev)
 
     # ------------------------------------------------------------------
     def _launch(self, sched) -> "_InFlightStep":
@@ -161,6 +175,8 @@ class LLMEngine:
                              ids_dev, ids_host, done)
 
     def _finish(self, step: "_InFlightStep") -> list[SequenceGroupOutput]:
+        if self._check_every_step:
+            self.check_device_errors()
         if step.ids_host is not None:
             step.done.synchronize()
             for seq, sg, tok in zip(step.sample_seqs, step.sample_groups, step.ids_host.tolist()):

@@ -60,6 +60,41 @@ def _check_int(name: str, t: torch.Tensor, dtype: torch.dtype, dim: int) -> None
 
 
 # ---------------------------------------------------------------------------
+# Device-side index errors
+# ---------------------------------------------------------------------------
+
+DEVICE_ERROR_NAMES = {
+    _hip.LV_DEVERR_BLOCK_ID: "block-table entry outside [0, num_cache_blocks)",
+    _hip.LV_DEVERR_SLOT: "slot_mapping entry >= num_blocks * block_size",
+}
+
+
+def device_errors(device: Optional[torch.device] = None, clear: bool = True) -> int:
+    """Bits (LV_DEVERR_*) of the out-of-range indices the kernels met on
+    `device` since the last clear; they were clamped (a block id outside the
+    cache read block 0, a slot past the cache was not written).  Waits for
+    the device.  lv_device_errors in include/litevllm_hip.h."""
+    lib = _hip.load()
+    flags = ctypes.c_uint32(0)
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        rc = lib.lv_device_errors(ctypes.byref(flags), 1 if clear else 0)
+    if rc not in (0, _hip.LV_ERR_DEVICE_INDEX):
+        _hip.check(rc, "lv_device_errors")
+    return int(flags.value)
+
+
+def check_device_errors(device: Optional[torch.device] = None) -> None:
+    """Raise RuntimeError if a kernel met an out-of-range index on `device`
+    (as the reference's torch indexing raises, layers/attention.py:80-84,
+    111-119); clears the report."""
+    bits = device_errors(device, clear=True)
+    if bits:
+        names = [n for b, n in DEVICE_ERROR_NAMES.items() if bits & b]
+        raise RuntimeError("litevllm kernels met out-of-range indices (clamped, results "
+                           "invalid): " + "; ".join(names))
+
+
+# ---------------------------------------------------------------------------
 # (2) KV scatter
 # ---------------------------------------------------------------------------
 

@@ -141,3 +141,30 @@ def test_sample_noalloc_refuses_requests_beyond_its_scratch():
     assert int(lib.lv_sample_workspace_size(1766, 151936)) > 4 << 20
     rc = lib.lv_sample_noalloc(None, 4, 100, 100, None, None, None, _hip.LV_BF16, None)
     assert rc == -1 and b"null pointer" in lib.lv_last_error()
+
+
+def test_device_error_report_host_side():
+    """lv_device_errors on a host without a GPU fails cleanly (LV_ERR_HIP,
+    flags zeroed) instead of crashing; the Python check names every bit it
+    is given."""
+    from litevllm import _hip, ops
+    lib = _hip.load()
+    flags = ctypes.c_uint32(0xdead)
+    rc = lib.lv_device_errors(ctypes.byref(flags), 1)
+    if rc == 0:
+        pytest.skip("a GPU is visible: the device report is covered by the -m gpu tests")
+    assert rc == -2 and flags.value == 0
+    assert b"lv_device_errors" in lib.lv_last_error()
+    assert lib.lv_device_errors(None, 0) == -2       # NULL flags_out is allowed
+    assert set(ops.DEVICE_ERROR_NAMES) == {_hip.LV_DEVERR_BLOCK_ID, _hip.LV_DEVERR_SLOT}
+
+
+def test_check_device_errors_message(monkeypatch):
+    from litevllm import _hip, ops
+    monkeypatch.setattr(ops, "device_errors", lambda device=None, clear=True: 0)
+    ops.check_device_errors()                         # nothing reported: no error
+    monkeypatch.setattr(ops, "device_errors",
+                        lambda device=None, clear=True: _hip.LV_DEVERR_BLOCK_ID |
+                        _hip.LV_DEVERR_SLOT)
+    with pytest.raises(RuntimeError, match="block-table entry.*slot_mapping entry"):
+        ops.check_device_errors()

@@ -57,3 +57,53 @@ def test_sample_noalloc_matches_lv_sample(device):
     want2, got2 = _both(lib, wide[:, :32000], sb2.temperature.to(device), sb2.uniform.to(device))
     assert torch.equal(got2, want2)
     assert torch.equal(got2[:20], sb2.planted[:20])
+
+
+def test_sample_noalloc_allocates_nothing_and_replays_in_a_graph(device):
+    """After a warm-up call (the scratch address lookup happens on the first
+    call on a device), a call changes neither torch's allocation count nor
+    the device's free memory, and the call captured in a HIP graph gives
+    lv_sample's ids on every replay, with new logits copied into the
+    captured input between replays and eager work in between."""
+    lib = _hip.load()
+    B, V = 64, 32000
+    batches = [workloads.sampler_batch(seed=s, rows=B, vocab=V) for s in (5, 6, 7, 8)]
+    logits = batches[0].logits.to(device)
+    temp = batches[0].temperature.to(device)
+    uni = batches[0].uniform.to(device)
+    got = torch.full((B,), -2, dtype=torch.int64, device=device)
+
+    def noalloc():
+        _hip.check(lib.lv_sample_noalloc(logits.data_ptr(), B, V, V, temp.data_ptr(),
+                                         uni.data_ptr(), got.data_ptr(), _hip.LV_BF16,
+                                         torch.cuda.current_stream().cuda_stream),
+                   "lv_sample_noalloc")
+
+    _say("lv_sample_noalloc: warm-up, then allocation check")
+    noalloc()
+    torch.cuda.synchronize()
+    alloc0, free0 = torch.cuda.memory_allocated(device), torch.cuda.mem_get_info(device)[0]
+    noalloc()
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated(device) == alloc0
+    assert torch.cuda.mem_get_info(device)[0] == free0
+
+    _say("lv_sample_noalloc: captured in a graph, 3 replays")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        noalloc()
+    for sb in batches[1:]:
+        logits.copy_(sb.logits.to(device))
+        temp.copy_(sb.temperature.to(device))
+        uni.copy_(sb.uniform.to(device))
+        got.fill_(-2)
+        g.replay()
+        torch.cuda.synchronize()
+        first = got.cpu()
+        want, _ = _both(lib, logits, temp, uni)     # eager lv_sample (+ noalloc) between
+        got.fill_(-2)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(first, want) and torch.equal(got.cpu(), want)
+        assert torch.equal(want[:B // 2], sb.planted[:B // 2])
+    del g
