@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import json
 import math
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -388,6 +389,29 @@ def test_pack_random(device, seed):
     ref = opack.expand_descriptors(descs, blocks, toks, bs, mb, device_tokens=dev_toks)
     for k in ref:
         assert np.array_equal(got[k], ref[k]), k
+
+
+sys.path.insert(0, str(Path(__file__).parent / "golden"))
+import packing_fixture  # noqa: E402
+
+
+def test_pack_reference_fixtures(device):
+    """Every schedule whose packed arrays the reference's own
+    ModelRunner.prepare_inputs wrote (tests/golden/reference_packing.npz:
+    40 decode-only and 40 prefill-only batches, block tables from its
+    BlockManager, block sizes 8/16/32), replayed through lv_pack_inputs:
+    bit-exact."""
+    cases = packing_fixture.load_cases()
+    _say(f"pack: {len(cases)} reference prepare_inputs fixtures")
+    for case in cases:
+        descs, blocks, toks = opack.descriptors_from_records(case["seqs"])
+        mb = max(len(s.block_ids) for s in case["seqs"])
+        got = _pack_on_gpu(device, descs, blocks, toks, case["block_size"], mb)
+        for k in ("input_ids", "positions", "slot_mapping"):
+            assert np.array_equal(got[k], case[k]), (case["name"], k)
+        if not case["is_prefill"]:
+            assert np.array_equal(got["block_tables"], case["block_tables"]), case["name"]
+            assert np.array_equal(got["context_lens"], case["context_lens"]), case["name"]
 
 
 def test_pack_config3(device):

@@ -4,6 +4,7 @@ vs descriptor expansion, closed-form invariants."""
 from __future__ import annotations
 
 import json
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -115,3 +116,41 @@ def test_device_token_indirection():
     assert got["input_ids"].tolist() == [777, 100, 101, 102]
     assert got["positions"].tolist() == [5, 0, 1, 2]
     assert got["slot_mapping"].tolist() == [4 * 16 + 5, 7 * 16, 7 * 16 + 1, 7 * 16 + 2]
+
+
+# ---------------------------------------------------------------------------
+# Pinned to the reference itself: 80 decode-only and prefill-only schedules
+# whose packed arrays the reference's ModelRunner.prepare_inputs wrote
+# (tests/golden/make_packing_fixtures.py, block tables from its BlockManager).
+# ---------------------------------------------------------------------------
+
+sys.path.insert(0, str(Path(__file__).parent / "golden"))
+import packing_fixture  # noqa: E402
+
+REF_CASES = packing_fixture.load_cases()
+
+
+def test_reference_fixture_covers_both_batch_kinds_and_the_slot0_rule():
+    kinds = {c["is_prefill"] for c in REF_CASES}
+    assert kinds == {True, False} and len(REF_CASES) >= 50
+    # some sequence of some case writes past its table (slot 0)
+    assert any(any(len(s.block_ids) * c["block_size"] < s.total_len for s in c["seqs"])
+               for c in REF_CASES)
+
+
+@pytest.mark.parametrize("case", REF_CASES, ids=lambda c: c["name"])
+def test_oracle_matches_reference_prepare_inputs(case):
+    bs = case["block_size"]
+    lit = prepare_inputs_literal(case["seqs"], bs)
+    descs, blocks, toks = descriptors_from_records(case["seqs"])
+    mb = max(len(s.block_ids) for s in case["seqs"])
+    got = expand_descriptors(descs, blocks, toks, bs, mb)
+    for key in ("input_ids", "positions", "slot_mapping"):
+        assert lit[key] == case[key].tolist(), key
+        assert np.array_equal(got[key], case[key]), key
+    assert lit["is_prefill"] == case["is_prefill"]
+    if not case["is_prefill"]:
+        assert np.array_equal(got["block_tables"], case["block_tables"])
+        assert np.array_equal(got["context_lens"], case["context_lens"])
+        assert lit["block_tables"] == case["block_tables"].tolist()
+        assert lit["context_lens"] == case["context_lens"].tolist()
