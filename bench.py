@@ -50,6 +50,21 @@ def _cpu_threads() -> int:
         return os.cpu_count() or 1
 
 
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+TRAFFIC_SOURCE = ("profiles/traffic.json: HBM bytes per call from separate rocprofv3 --pmc "
+                  "FETCH_SIZE / WRITE_SIZE runs of this workload, scaled by the plain-copy "
+                  "calibration (not measured in this run)")
+
+
 def _time_gpu(fn, steps: int, warmup: int):
     """Run fn warmup+steps times; return (total ms over the timed steps,
     per-step event durations in ms)."""
@@ -139,7 +154,7 @@ def bench_decode(args):
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": _traffic("decode"),
+            "traffic": _traffic("decode"), "traffic_source": TRAFFIC_SOURCE,
             "algorithmic_bytes": nbytes, "avg_launch_us": round(kern_ms * 1e3, 2),
         },
     }
@@ -168,7 +183,7 @@ def cpu_baseline_decode(cpu_batch, n_seqs: int = 64):
                           cpu_batch.scale)
     return {
         "value": round(decode_bytes(sub) / secs / 1e9, 3), "unit": "GB/s (algorithmic, bf16 bytes)",
-        "cores": threads, "kind": "port",
+        "cores": threads, "cpu_model": _cpu_model(), "kind": "port",
         "sample": f"config2 sequences 0..{n_seqs - 1} (sum ctx {int(ctx.sum())}), fp32 "
                   f"_decode_fast restatement (oracle.attention.decode_attention), median of 5 "
                   f"after 1 warmup: {secs * 1e3:.1f} ms",
@@ -205,7 +220,7 @@ def bench_sampler(args):
                              "the roofline figures are over the whole call)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": _traffic("sampler"),
+                     "traffic": _traffic("sampler"), "traffic_source": TRAFFIC_SOURCE,
                      "algorithmic_bytes": nbytes, "avg_launch_us": round(kern_ms * 1e3, 2)},
     }
     if not args.no_cpu_baseline:
@@ -218,7 +233,7 @@ def bench_sampler(args):
                                                  sb.temperature[128:144].numpy(),
                                                  sb.uniform[128:144].numpy())))
         res["cpu_baseline"] = {"value": round(32 / secs, 2), "unit": "sampled rows/s",
-                               "cores": 1, "kind": "port",
+                               "cores": 1, "cpu_model": _cpu_model(), "kind": "port",
                                "sample": "16 greedy + 16 temperature rows of config4 through "
                                          "oracle.sampler (numpy argmax, C inverse-CDF), median of 5"}
         del x, t
@@ -297,6 +312,105 @@ def bench_mixed(args):
                 "this workload with --no-secondary)",
     }
     return result
+
+
+def mixed_kernel_rooflines(steps: int = 20, warmup: int = 5):
+    """Config 3 split into its kernels, each bracketed by HIP events on the
+    launch stream, in step order: packing, KV scatter, the prefill-chunk
+    rows (lv_paged_attention on the chunk sequences alone: the MFMA chunk
+    kernel) and the decode rows (lv_paged_attention on the decode sequences
+    alone: the persistent decode kernel + its reduce).  Returns the three
+    roofline entries of the bench line's `secondary` list."""
+    import torch
+    from litevllm import ops, workloads
+    dev = torch.device("cuda:0")
+    step_cpu = workloads.mixed_step(seed=0)
+    b = step_cpu.batch.to(dev)
+    key, value = step_cpu.key.to(dev), step_cpu.value.to(dev)
+    descs, block_ids = step_cpu.descs.to(dev), step_cpu.block_ids.to(dev)
+    token_ids = step_cpu.token_ids.to(dev)
+    T = step_cpu.token_ids.shape[0]
+    mb = b.block_tables.shape[1]
+    nd = b.num_decodes
+    H, D = b.query.shape[1], b.query.shape[2]
+    hkv = b.key_cache.shape[2]
+    packed = ops.pack_inputs(descs, block_ids, token_ids, T, 16, mb)
+    q_c, q_d = b.query[nd:], b.query[:nd]
+    out_c, out_d = torch.empty_like(q_c), torch.empty_like(q_d)
+    cu_c = (packed["cu_seqlens"][nd:] - nd).contiguous()
+    segs = ("pack", "scatter", "chunks", "decodes")
+    evs = {k: [] for k in segs}
+
+    def run(record):
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(5)] if record else None
+        if record:
+            marks[0].record()
+        p = ops.pack_inputs(descs, block_ids, token_ids, T, 16, mb, out=packed)
+        if record:
+            marks[1].record()
+        ops.kv_scatter(key, value, b.key_cache, b.value_cache, p["slot_mapping"])
+        if record:
+            marks[2].record()
+        ops.paged_attention(q_c, b.key_cache, b.value_cache, p["block_tables"][nd:],
+                            p["context_lens"][nd:], scale=b.scale, cu_seqlens=cu_c,
+                            num_decodes=0, max_query_len=b.max_query_len, out=out_c)
+        if record:
+            marks[3].record()
+        ops.paged_attention(q_d, b.key_cache, b.value_cache, p["block_tables"][:nd],
+                            p["context_lens"][:nd], scale=b.scale, out=out_d)
+        if record:
+            marks[4].record()
+            for i, k in enumerate(segs):
+                evs[k].append((marks[i], marks[i + 1]))
+
+    for _ in range(warmup):
+        run(False)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        run(True)
+    torch.cuda.synchronize()
+    us = {k: statistics.mean(a.elapsed_time(c) for a, c in v) * 1e3 for k, v in evs.items()}
+    cu_cpu = step_cpu.batch.cu_seqlens.tolist()
+    ctx_cpu = step_cpu.batch.context_lens.tolist()
+    flops = 0
+    for i in range(nd, len(ctx_cpu)):
+        L = cu_cpu[i + 1] - cu_cpu[i]
+        flops += 4 * H * D * (L * (ctx_cpu[i] - L) + L * (L + 1) // 2)
+    scatter_bytes = T * hkv * D * 2 * 2 * b.key_cache.element_size() + T * 8
+    sub = workloads.PagedBatch(step_cpu.batch.query[:nd], step_cpu.batch.key_cache,
+                               step_cpu.batch.value_cache, step_cpu.batch.block_tables[:nd],
+                               step_cpu.batch.context_lens[:nd],
+                               step_cpu.batch.cu_seqlens[:nd + 1], nd, 1, step_cpu.batch.scale)
+    dec_bytes = decode_bytes(sub)
+    wl = ("config3 mixed step (192 decodes ctx U[256,4096] + 15 chunks x 512 at offset "
+          "U[0,3072], 200k-slot cache, bf16), kernels timed one by one in step order, "
+          f"{steps} steps after {warmup} warmup")
+
+    def hbm(nbytes, t_us):
+        a = nbytes / (t_us * 1e-6) / 1e9
+        return {"bound": "hbm", "achieved": round(a, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(a / HBM_PEAK_GBPS, 4), "traffic": None,
+                "algorithmic_bytes": int(nbytes), "avg_launch_us": round(t_us, 2)}
+    tf = flops / (us["chunks"] * 1e-6) / 1e12
+    return [
+        {"metric": "KV scatter HBM GB/s (config 3)", "kernel": "lv_kv_scatter (kv_scatter_kernel)",
+         "value": round(scatter_bytes / (us["scatter"] * 1e-6) / 1e9, 1), "unit": "GB/s",
+         "roofline": hbm(scatter_bytes, us["scatter"]), "config": wl,
+         "pack_us": round(us["pack"], 2)},
+        {"metric": "prefill-chunk attention MFMA TFLOP/s (config 3)",
+         "kernel": "lv_paged_attention chunk rows (attn_chunk_mfma_kernel)",
+         "value": round(tf, 1), "unit": "TFLOP/s",
+         "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                      "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                      "traffic": None, "algorithmic_flops": flops,
+                      "avg_launch_us": round(us["chunks"], 2)},
+         "config": wl},
+        {"metric": "paged-decode attn HBM GB/s (config 3 decode rows)",
+         "kernel": "lv_paged_attention decode rows (attn_decode_persistent_kernel + "
+                   "attn_persist_reduce_kernel)",
+         "value": round(dec_bytes / (us["decodes"] * 1e-6) / 1e9, 1), "unit": "GB/s",
+         "roofline": hbm(dec_bytes, us["decodes"]), "config": wl},
+    ]
 
 
 def bench_e2e(args):
@@ -442,7 +556,7 @@ def bench_e2e(args):
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": _traffic("e2e_decode"),
+            "traffic": _traffic("e2e_decode"), "traffic_source": TRAFFIC_SOURCE,
             "algorithmic_bytes": int(probe["bytes"] / max(len(durs), 1)),
             "avg_launch_us": round(attn_ms * 1e3 / max(len(durs), 1), 2),
             "launches": len(durs),
@@ -458,12 +572,26 @@ def bench_e2e(args):
             result["cpu_baseline"], result["parity"] = cpu_baseline_e2e(
                 cpu_state, cpu_cfg, prompts, streams)
         return result
+    # Every hot-path kernel's roofline beside the headline, in this run:
+    # config 2 decode attention, config 3 split into its kernels, config 4
+    # sampler (all HIP events on the launch stream).
     _log("e2e: config-2 decode-attention microbench")
     dec = bench_decode(argparse.Namespace(steps=50, warmup=10, no_cpu_baseline=True))
-    result["secondary"] = {
+    secondary = [{
         "metric": "paged-decode attn HBM GB/s (config 2, 50 launches after 10 warmup)",
+        "kernel": dec["config"]["kernel"],
         "value": dec["value"], "unit": dec["unit"], "roofline": dec["roofline"],
-        "config": dec["config"]["workload"]}
+        "config": dec["config"]["workload"]}]
+    _log("e2e: config-3 kernels")
+    secondary += mixed_kernel_rooflines()
+    _log("e2e: config-4 sampler")
+    smp = bench_sampler(argparse.Namespace(steps=50, warmup=10, no_cpu_baseline=True,
+                                           sampler_rows="config4"))
+    secondary.append({
+        "metric": "fused sampler HBM GB/s (config 4, 50 calls after 10 warmup)",
+        "kernel": smp["config"]["kernel"], "value": smp["roofline"]["achieved"], "unit": "GB/s",
+        "roofline": smp["roofline"], "config": smp["config"]["workload"]})
+    result["secondary"] = secondary
     if not args.no_cpu_baseline:
         result["cpu_baseline"], result["parity"] = cpu_baseline_e2e(
             cpu_state, cpu_cfg, prompts, streams)
@@ -518,7 +646,7 @@ def cpu_baseline_e2e(state, model_config, prompts, streams, n_seqs: int = 8, n_s
         check(logits, t + 1)
         pos = [x + 1 for x in pos]
     base = {"value": round(n_seqs * n_steps / max(secs, 1e-9), 2), "unit": "output tok/s",
-            "cores": threads, "kind": "port",
+            "cores": threads, "cpu_model": _cpu_model(), "kind": "port",
             "sample": f"config5 prompts 0..{n_seqs - 1} ({sum(map(len, prompts[:n_seqs]))} prompt "
                       f"tokens, prefill untimed), {n_steps} batched greedy decode steps of "
                       f"oracle.model.OracleDecoder (fp32 restatement of the reference model "

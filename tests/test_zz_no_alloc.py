@@ -90,7 +90,10 @@ def test_sample_noalloc_allocates_nothing_and_replays_in_a_graph(device):
 
     _say("lv_sample_noalloc: captured in a graph, 3 replays")
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # inference mode, as the engine captures its graphs: capture_begin
+    # updates the CUDA generator's state, which an earlier engine run in the
+    # same process may have created as an inference tensor
+    with torch.inference_mode(), torch.cuda.graph(g):
         noalloc()
     for sb in batches[1:]:
         logits.copy_(sb.logits.to(device))
