@@ -87,6 +87,32 @@ def _time_gpu(fn, steps: int, warmup: int):
     return t_start.elapsed_time(t_end), [a.elapsed_time(b) for a, b in evs]
 
 
+def _time_back_to_back(fn, calls: int = 20, reps: int = 5, warmup: int = 3) -> float:
+    """Average time per call (ms) of `calls` back-to-back launches of fn
+    between one pair of HIP events on the launch stream (median of reps):
+    the kernels' own duration, without the cost of an event pair around
+    every call (2-6 us on this part, a large share of a 10-25 us kernel)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(calls):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) / calls)
+    return statistics.median(ts)
+
+
+B2B_NOTE = ("avg_launch_us: 20 back-to-back calls between one pair of HIP events on the launch "
+            "stream (median of 5); per_call_event_us: one event pair around every call")
+
+
 def _median_cpu(fn, reps: int = 5) -> float:
     fn()  # warmup
     ts = []
@@ -138,7 +164,7 @@ def bench_decode(args):
 
     total_ms, per = _time_gpu(step, args.steps, args.warmup)
     nbytes = decode_bytes(cpu_batch)
-    kern_ms = statistics.mean(per)
+    kern_ms = _time_back_to_back(step)
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
     result = {
         "value": round(achieved, 1),
@@ -156,6 +182,7 @@ def bench_decode(args):
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": _traffic("decode"), "traffic_source": TRAFFIC_SOURCE,
             "algorithmic_bytes": nbytes, "avg_launch_us": round(kern_ms * 1e3, 2),
+            "per_call_event_us": round(statistics.mean(per) * 1e3, 2), "timing": B2B_NOTE,
         },
     }
     if not args.no_cpu_baseline:
@@ -203,11 +230,11 @@ def bench_sampler(args):
         temp = torch.full_like(temp, 0.75)
     uni = sb.uniform.to(dev)
     out = torch.empty(logits.shape[0], dtype=torch.int64, device=dev)
-    total_ms, per = _time_gpu(lambda: ops.sample(logits, temp, uni, out=out), args.steps,
-                              args.warmup)
+    call = lambda: ops.sample(logits, temp, uni, out=out)
+    total_ms, per = _time_gpu(call, args.steps, args.warmup)
     B, V = logits.shape
     nbytes = B * V * logits.element_size() + B * (4 + 4 + 8)
-    kern_ms = statistics.mean(per)
+    kern_ms = _time_back_to_back(call)
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
     res = {
         "value": round(B / (kern_ms * 1e-3), 1), "unit": "sampled rows/s",
@@ -221,7 +248,9 @@ def bench_sampler(args):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": _traffic("sampler"), "traffic_source": TRAFFIC_SOURCE,
-                     "algorithmic_bytes": nbytes, "avg_launch_us": round(kern_ms * 1e3, 2)},
+                     "algorithmic_bytes": nbytes, "avg_launch_us": round(kern_ms * 1e3, 2),
+                     "per_call_event_us": round(statistics.mean(per) * 1e3, 2),
+                     "timing": B2B_NOTE},
     }
     if not args.no_cpu_baseline:
         from oracle import sampler as osamp
@@ -370,6 +399,10 @@ def mixed_kernel_rooflines(steps: int = 20, warmup: int = 5):
         run(True)
     torch.cuda.synchronize()
     us = {k: statistics.mean(a.elapsed_time(c) for a, c in v) * 1e3 for k, v in evs.items()}
+    # the scatter (~10 us) timed back to back as well: the event pair around
+    # each in-step call costs a large share of it
+    scatter_b2b = _time_back_to_back(
+        lambda: ops.kv_scatter(key, value, b.key_cache, b.value_cache, packed["slot_mapping"])) * 1e3
     cu_cpu = step_cpu.batch.cu_seqlens.tolist()
     ctx_cpu = step_cpu.batch.context_lens.tolist()
     flops = 0
@@ -386,30 +419,36 @@ def mixed_kernel_rooflines(steps: int = 20, warmup: int = 5):
           "U[0,3072], 200k-slot cache, bf16), kernels timed one by one in step order, "
           f"{steps} steps after {warmup} warmup")
 
-    def hbm(nbytes, t_us):
+    def hbm(nbytes, t_us, in_step_us, timing):
         a = nbytes / (t_us * 1e-6) / 1e9
         return {"bound": "hbm", "achieved": round(a, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(a / HBM_PEAK_GBPS, 4), "traffic": None,
-                "algorithmic_bytes": int(nbytes), "avg_launch_us": round(t_us, 2)}
+                "algorithmic_bytes": int(nbytes), "avg_launch_us": round(t_us, 2),
+                "in_step_event_us": round(in_step_us, 2), "timing": timing}
+    in_step = ("avg_launch_us: one pair of HIP events around each call in the step "
+               f"({steps} steps)")
     tf = flops / (us["chunks"] * 1e-6) / 1e12
     return [
         {"metric": "KV scatter HBM GB/s (config 3)", "kernel": "lv_kv_scatter (kv_scatter_kernel)",
-         "value": round(scatter_bytes / (us["scatter"] * 1e-6) / 1e9, 1), "unit": "GB/s",
-         "roofline": hbm(scatter_bytes, us["scatter"]), "config": wl,
-         "pack_us": round(us["pack"], 2)},
+         "value": round(scatter_bytes / (scatter_b2b * 1e-6) / 1e9, 1), "unit": "GB/s",
+         "roofline": hbm(scatter_bytes, scatter_b2b, us["scatter"],
+                         "avg_launch_us: 20 back-to-back calls between one pair of HIP events "
+                         "(median of 5); in_step_event_us: an event pair around the call in "
+                         "the step"),
+         "config": wl, "pack_in_step_event_us": round(us["pack"], 2)},
         {"metric": "prefill-chunk attention MFMA TFLOP/s (config 3)",
          "kernel": "lv_paged_attention chunk rows (attn_chunk_mfma_kernel)",
          "value": round(tf, 1), "unit": "TFLOP/s",
          "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                       "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
                       "traffic": None, "algorithmic_flops": flops,
-                      "avg_launch_us": round(us["chunks"], 2)},
+                      "avg_launch_us": round(us["chunks"], 2), "timing": in_step},
          "config": wl},
         {"metric": "paged-decode attn HBM GB/s (config 3 decode rows)",
          "kernel": "lv_paged_attention decode rows (attn_decode_persistent_kernel + "
                    "attn_persist_reduce_kernel)",
          "value": round(dec_bytes / (us["decodes"] * 1e-6) / 1e9, 1), "unit": "GB/s",
-         "roofline": hbm(dec_bytes, us["decodes"]), "config": wl},
+         "roofline": hbm(dec_bytes, us["decodes"], us["decodes"], in_step), "config": wl},
     ]
 
 
@@ -436,7 +475,19 @@ def bench_e2e(args):
     # graphs on, one decode step in SAMPLE_EVERY runs eagerly (same kernels,
     # same data) and is the timing sample; the others replay graphs.
     SAMPLE_EVERY = 32
-    probe = {"on": False, "meta": None, "durs": [], "bytes": 0, "decode_steps": 0}
+    probe = {"on": False, "meta": None, "durs": [], "bytes": 0, "decode_steps": 0,
+             "saved": [], "shared": {}}
+    import ctypes
+    _hiprt = ctypes.CDLL("libamdhip64.so")
+    _hiprt.hipMemcpyAsync.restype = ctypes.c_int
+    _hiprt.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_int, ctypes.c_void_p]
+
+    def hip_memcpy_d2d(dst, src, n):
+        # stream-ordered after the call that read these inputs (kind 3:
+        # device to device); no host synchronisation
+        if _hiprt.hipMemcpyAsync(dst, src, n, 3, torch.cuda.current_stream().cuda_stream) != 0:
+            raise RuntimeError("hipMemcpyAsync failed")
     orig_exec = mr.ModelRunner.execute_model
     orig_accepts = mr.DecodeGraphs.accepts
     lib = _hip.load()
@@ -457,6 +508,68 @@ def bench_e2e(args):
         probe["meta"] = meta
         return orig_exec(self, meta)
 
+    # Graph-replay timing of the same calls: the serving loop runs decode
+    # steps as HIP-graph replays, where the call's kernels follow each other
+    # without the eager launch gaps.  Each sampled call's inputs (query, block
+    # tables, context lengths, shared-prefix plan; the layer's KV cache stays
+    # in place) are copied aside; after the timed region each call is
+    # captured as a one-call graph on its saved inputs and replayed, and the
+    # second replay is timed with HIP events.
+    def dev_copy(ptr, nbytes):
+        t = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device="cuda")
+        if ptr and nbytes:
+            hip_memcpy_d2d(t.data_ptr(), ptr, int(nbytes))
+        return t
+
+    def save_call(name, args, nbytes):
+        a = list(args)
+        H, D = a[13], a[15]
+        B, mb, T = a[9], a[6], a[11]
+        step_key = probe["decode_steps"]
+        shared = probe["shared"].get(step_key)
+        if shared is None:      # tables, lengths and plan: the same for every layer of a step
+            shared = {"bt": dev_copy(a[5], B * mb * 4), "ctx": dev_copy(a[8], B * 4)}
+            if name == "lv_paged_attention_prefix":
+                shared["pb"] = dev_copy(a[22], a[10] * 4)
+                shared["pi"] = dev_copy(a[23], a[24] * 16)
+                shared["pm"] = dev_copy(a[25], a[26] * 4)
+            probe["shared"] = {step_key: shared}
+        q = dev_copy(a[0], T * a[1] * (4 if a[-2] == _hip.LV_F32 else 2))
+        probe["saved"].append((name, a, shared, q, nbytes))
+
+    REPLAY_COPIES = 8
+
+    def replay_saved():
+        times, nbytes = [], 0
+        for name, a, sh, q, nb in probe["saved"]:
+            a = list(a)
+            out = torch.empty(max(a[11] * a[19] * (4 if a[-2] == _hip.LV_F32 else 2), 1),
+                              dtype=torch.uint8, device="cuda")
+            ws = torch.zeros(max(a[21], 1), dtype=torch.uint8, device="cuda")
+            a[0], a[5], a[8], a[18], a[20] = q.data_ptr(), sh["bt"].data_ptr(), \
+                sh["ctx"].data_ptr(), out.data_ptr(), ws.data_ptr()
+            if name == "lv_paged_attention_prefix":
+                pws = torch.zeros(max(a[28], 1), dtype=torch.uint8, device="cuda")
+                a[22], a[23], a[25], a[27] = sh["pb"].data_ptr(), sh["pi"].data_ptr(), \
+                    sh["pm"].data_ptr(), pws.data_ptr()
+            fn = orig_c[name]
+            g = torch.cuda.CUDAGraph()
+            with torch.inference_mode(), torch.cuda.graph(g):
+                a[-1] = torch.cuda.current_stream().cuda_stream
+                for _ in range(REPLAY_COPIES):
+                    _hip.check(fn(*a), name)
+            g.replay()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / REPLAY_COPIES)
+            nbytes += nb
+            del g
+        return times, nbytes
+
     def c_probe(name):
         fn = orig_c[name]
 
@@ -470,7 +583,10 @@ def bench_e2e(args):
             rc = fn(*args)
             e1.record()
             probe["durs"].append((e0, e1))
-            probe["bytes"] += step_bytes(meta)
+            nb = step_bytes(meta)
+            probe["bytes"] += nb
+            if len(probe["saved"]) < 32 * mc["num_hidden_layers"]:
+                save_call(name, args, nb)
             return rc
         return call
 
@@ -523,6 +639,10 @@ def bench_e2e(args):
         setattr(lib, n, fn)
     mr.DecodeGraphs.accepts = orig_accepts
     durs = [a.elapsed_time(b) for a, b in probe["durs"]]
+    _log(f"e2e: graph replays of the {len(probe['saved'])} sampled attention calls")
+    gdurs, gbytes = replay_saved()
+    probe["saved"].clear()
+    probe["shared"].clear()
     cpu_state = cpu_cfg = None
     by_prompt = {tuple(o.prompt_token_ids): list(o.output_token_ids) for o in outs}
     streams = [by_prompt[tuple(p)] for p in prompts[:8]]
@@ -531,7 +651,9 @@ def bench_e2e(args):
                      for k, v in eng.model_runner.model.state_dict().items()}
         cpu_cfg = eng.config.model_config
     attn_ms = sum(durs)
-    achieved = probe["bytes"] / (attn_ms * 1e-3) / 1e9 if durs else 0.0
+    achieved_eager = probe["bytes"] / (attn_ms * 1e-3) / 1e9 if durs else 0.0
+    gattn_ms = sum(gdurs)
+    achieved = gbytes / (gattn_ms * 1e-3) / 1e9 if gdurs else 0.0
     result = {
         "value": round(n_out / wall, 1), "unit": "output tok/s",
         "ms_per_step": round(wall * 1e3 / args.steps, 2),
@@ -557,9 +679,23 @@ def bench_e2e(args):
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": _traffic("e2e_decode"), "traffic_source": TRAFFIC_SOURCE,
-            "algorithmic_bytes": int(probe["bytes"] / max(len(durs), 1)),
-            "avg_launch_us": round(attn_ms * 1e3 / max(len(durs), 1), 2),
-            "launches": len(durs),
+            "algorithmic_bytes": int(gbytes / max(len(gdurs), 1)),
+            "avg_launch_us": round(gattn_ms * 1e3 / max(len(gdurs), 1), 2),
+            "launches": len(gdurs),
+            "timing": ("graph replay (as the serving loop runs decode steps) of every "
+                       "attention call of the sampled steps, on copies of that call's inputs "
+                       "(query, block tables, context lengths, shared-prefix plan; KV cache in "
+                       "place): after the timed region each call is captured 8 times back to "
+                       "back in one HIP graph, HIP events around the second replay, time / 8 "
+                       "(a single bracketed call adds ~10 us of launch and event overhead that "
+                       "a call inside the decode-step graph does not pay)"),
+            "eager": {
+                "achieved": round(achieved_eager, 1),
+                "frac": round(achieved_eager / HBM_PEAK_GBPS, 4),
+                "avg_launch_us": round(attn_ms * 1e3 / max(len(durs), 1), 2),
+                "launches": len(durs),
+                "timing": "HIP events around each call in the eagerly run sample steps "
+                          "(includes the eager launch gaps between the call's kernels)"},
             "attention_share_of_wall_est": round(
                 attn_ms / max(len(durs), 1) * 1e-3 * mc["num_hidden_layers"]
                 * probe["decode_steps"] / wall, 4) if not args.eager else round(attn_ms * 1e-3 / wall, 4),
