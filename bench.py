@@ -419,10 +419,11 @@ def mixed_kernel_rooflines(steps: int = 20, warmup: int = 5):
           "U[0,3072], 200k-slot cache, bf16), kernels timed one by one in step order, "
           f"{steps} steps after {warmup} warmup")
 
-    def hbm(nbytes, t_us, in_step_us, timing):
+    def hbm(nbytes, t_us, in_step_us, timing, traffic_key):
         a = nbytes / (t_us * 1e-6) / 1e9
         return {"bound": "hbm", "achieved": round(a, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(a / HBM_PEAK_GBPS, 4), "traffic": None,
+                "frac": round(a / HBM_PEAK_GBPS, 4), "traffic": _traffic(traffic_key),
+                "traffic_source": TRAFFIC_SOURCE,
                 "algorithmic_bytes": int(nbytes), "avg_launch_us": round(t_us, 2),
                 "in_step_event_us": round(in_step_us, 2), "timing": timing}
     in_step = ("avg_launch_us: one pair of HIP events around each call in the step "
@@ -434,21 +435,23 @@ def mixed_kernel_rooflines(steps: int = 20, warmup: int = 5):
          "roofline": hbm(scatter_bytes, scatter_b2b, us["scatter"],
                          "avg_launch_us: 20 back-to-back calls between one pair of HIP events "
                          "(median of 5); in_step_event_us: an event pair around the call in "
-                         "the step"),
+                         "the step", "scatter_config3"),
          "config": wl, "pack_in_step_event_us": round(us["pack"], 2)},
         {"metric": "prefill-chunk attention MFMA TFLOP/s (config 3)",
          "kernel": "lv_paged_attention chunk rows (attn_chunk_mfma_kernel)",
          "value": round(tf, 1), "unit": "TFLOP/s",
          "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                       "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                      "traffic": None, "algorithmic_flops": flops,
+                      "traffic": _traffic("chunk_config3"), "traffic_source": TRAFFIC_SOURCE,
+                      "algorithmic_flops": flops,
                       "avg_launch_us": round(us["chunks"], 2), "timing": in_step},
          "config": wl},
         {"metric": "paged-decode attn HBM GB/s (config 3 decode rows)",
          "kernel": "lv_paged_attention decode rows (attn_decode_persistent_kernel + "
                    "attn_persist_reduce_kernel)",
          "value": round(dec_bytes / (us["decodes"] * 1e-6) / 1e9, 1), "unit": "GB/s",
-         "roofline": hbm(dec_bytes, us["decodes"], us["decodes"], in_step), "config": wl},
+         "roofline": hbm(dec_bytes, us["decodes"], us["decodes"], in_step,
+                         "decode_rows_config3"), "config": wl},
     ]
 
 
@@ -639,8 +642,11 @@ def bench_e2e(args):
         setattr(lib, n, fn)
     mr.DecodeGraphs.accepts = orig_accepts
     durs = [a.elapsed_time(b) for a, b in probe["durs"]]
-    _log(f"e2e: graph replays of the {len(probe['saved'])} sampled attention calls")
-    gdurs, gbytes = replay_saved()
+    if args.no_graph_timing:          # (keeps a kernel trace of this run to the serving run)
+        gdurs, gbytes = [], 0
+    else:
+        _log(f"e2e: graph replays of the {len(probe['saved'])} sampled attention calls")
+        gdurs, gbytes = replay_saved()
     probe["saved"].clear()
     probe["shared"].clear()
     cpu_state = cpu_cfg = None
@@ -653,7 +659,9 @@ def bench_e2e(args):
     attn_ms = sum(durs)
     achieved_eager = probe["bytes"] / (attn_ms * 1e-3) / 1e9 if durs else 0.0
     gattn_ms = sum(gdurs)
-    achieved = gbytes / (gattn_ms * 1e-3) / 1e9 if gdurs else 0.0
+    if not gdurs:                      # --no-graph-timing: the eager figure only
+        gdurs, gattn_ms, gbytes = [0.0] * len(durs), attn_ms, probe["bytes"]
+    achieved = gbytes / (gattn_ms * 1e-3) / 1e9 if gattn_ms else 0.0
     result = {
         "value": round(n_out / wall, 1), "unit": "output tok/s",
         "ms_per_step": round(wall * 1e3 / args.steps, 2),
@@ -682,7 +690,9 @@ def bench_e2e(args):
             "algorithmic_bytes": int(gbytes / max(len(gdurs), 1)),
             "avg_launch_us": round(gattn_ms * 1e3 / max(len(gdurs), 1), 2),
             "launches": len(gdurs),
-            "timing": ("graph replay (as the serving loop runs decode steps) of every "
+            "timing": "HIP events around each eager call (--no-graph-timing)"
+            if args.no_graph_timing else
+                      ("graph replay (as the serving loop runs decode steps) of every "
                        "attention call of the sampled steps, on copies of that call's inputs "
                        "(query, block tables, context lengths, shared-prefix plan; KV cache in "
                        "place): after the timed region each call is captured 8 times back to "
@@ -836,6 +846,9 @@ def main() -> int:
                          "all greedy, or all at T = 0.75 (same logits; a diagnostic)")
     ap.add_argument("--eager", action="store_true",
                     help="e2e: no HIP graphs for decode steps")
+    ap.add_argument("--no-graph-timing", action="store_true",
+                    help="e2e: skip the graph replays of the sampled attention calls (the "
+                         "roofline then holds the eager per-call figure; for kernel traces)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="e2e: skip the config-2 decode-attention microbench; mixed: skip "
                          "the chunk-rows-alone timing")

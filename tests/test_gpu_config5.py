@@ -10,7 +10,7 @@ HIP graphs on), fed config-5 prompts 0-7 of ``workloads.e2e_prompts(seed=0)``
 The fp32 CPU oracle decoder (``oracle.model.OracleDecoder``, the reference's
 model path restated, reference models/qwen3.py:24-195, engine
 llm_engine.py:102-149) gets the same weights and is teacher-forced on the
-engine's own token stream, so every one of the 8 x 24 generated tokens is
+engine's own token stream, so every one of the 8 x 64 generated tokens is
 checked, not only a prefix up to the first near-tie:
 
 * where the oracle's top-2 logit margin is at least MARGIN, the engine's
@@ -33,7 +33,8 @@ headroom.  Rounding can swap the argmax only between two logits closer than
 twice the per-logit error (<= 0.084 at the measured max-abs); MARGIN = 0.1
 covers that, so a token that differs where the margin is larger is a real
 error.  The top-2 margin of these random-weight logits is often small: 56
-of the 192 tokens cleared MARGIN when measured; the test asks for 40.
+of the first 192 tokens cleared MARGIN when measured; the test asks that at
+least a fifth of the 512 do (so the argmax check has teeth).
 """
 
 from __future__ import annotations
@@ -46,7 +47,7 @@ from oracle.model import OracleDecoder
 
 pytestmark = pytest.mark.gpu
 
-N_OUT = 24
+N_OUT = 64
 MARGIN = 0.1
 LOGIT_MAX_ABS = 0.1
 LOGIT_REL_L2 = 0.03
@@ -169,4 +170,4 @@ def test_config5_qwen3_shape_matches_cpu_oracle(device, monkeypatch):
             logits = oracle.decode_batch([s[t] for s in streams], pos, kvs)
             pos = [x + 1 for x in pos]
     _say(f"tokens: {exact} exact argmax (margin >= {MARGIN}), {near} near-ties within {MARGIN}")
-    assert exact >= 40
+    assert exact >= N_OUT * 8 // 5

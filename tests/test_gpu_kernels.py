@@ -312,6 +312,39 @@ def test_sampler_config4(device):
     assert np.array_equal(got[half:].numpy(), ref)
 
 
+_SAMPLER_CHILD = r"""
+import sys, numpy as np, torch
+sys.path[:0] = sys.argv[1:3]
+from litevllm import ops, workloads
+sb = workloads.sampler_batch(seed=0)
+d = torch.device("cuda:0")
+ids = ops.sample(sb.logits.to(d), sb.temperature.to(d), sb.uniform.to(d)).cpu().numpy()
+np.save(sys.argv[3], ids)
+"""
+
+
+@pytest.mark.parametrize("per_cu", ["1", "3", "32"])
+def test_sampler_grid_knob_bit_identical(device, per_cu, tmp_path):
+    """LV_SAMPLER_WGS_PER_CU (workgroups of the items kernel per CU, read
+    once per process) only changes how segments are spread over
+    wavefronts: config 4's ids are bit-identical to this process's default
+    grid.  One child process per setting (the value is cached at first
+    use)."""
+    import os
+    import subprocess
+    import sys
+    _say(f"sampler LV_SAMPLER_WGS_PER_CU={per_cu} (child process)")
+    sb = workloads.sampler_batch(seed=0)
+    want = ops.sample(sb.logits.to(device), sb.temperature.to(device),
+                      sb.uniform.to(device)).cpu().numpy()
+    root = Path(__file__).resolve().parent.parent
+    out = tmp_path / "ids.npy"
+    env = dict(os.environ, LV_SAMPLER_WGS_PER_CU=per_cu)
+    subprocess.run([sys.executable, "-c", _SAMPLER_CHILD, str(root), str(root / "lite-vllm_amd"),
+                    str(out)], env=env, check=True, timeout=240)
+    assert np.array_equal(np.load(out), want)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("V", [1, 7, 511, 512, 513, 32000, 151936])
 def test_sampler_shapes(device, dtype, V):
