@@ -479,7 +479,7 @@ def bench_e2e(args):
     # same data) and is the timing sample; the others replay graphs.
     SAMPLE_EVERY = 32
     probe = {"on": False, "meta": None, "durs": [], "bytes": 0, "decode_steps": 0,
-             "saved": [], "shared": {}}
+             "saved": [], "shared": {}, "arena": None, "arena_at": 0}
     import ctypes
     _hiprt = ctypes.CDLL("libamdhip64.so")
     _hiprt.hipMemcpyAsync.restype = ctypes.c_int
@@ -518,15 +518,21 @@ def bench_e2e(args):
     # in place) are copied aside; after the timed region each call is
     # captured as a one-call graph on its saved inputs and replayed, and the
     # second replay is timed with HIP events.
+    # Copies go to one arena allocated before the timed region (no
+    # allocation inside it); a sample that does not fit is not saved.
     def dev_copy(ptr, nbytes):
-        t = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device="cuda")
+        n = (max(int(nbytes), 1) + 255) // 256 * 256
+        at = probe["arena_at"]
+        if at + n > probe["arena"].numel():
+            return None
+        t = probe["arena"][at:at + n]
+        probe["arena_at"] = at + n
         if ptr and nbytes:
             hip_memcpy_d2d(t.data_ptr(), ptr, int(nbytes))
         return t
 
     def save_call(name, args, nbytes):
         a = list(args)
-        H, D = a[13], a[15]
         B, mb, T = a[9], a[6], a[11]
         step_key = probe["decode_steps"]
         shared = probe["shared"].get(step_key)
@@ -538,6 +544,8 @@ def bench_e2e(args):
                 shared["pm"] = dev_copy(a[25], a[26] * 4)
             probe["shared"] = {step_key: shared}
         q = dev_copy(a[0], T * a[1] * (4 if a[-2] == _hip.LV_F32 else 2))
+        if q is None or any(v is None for v in shared.values()):
+            return
         probe["saved"].append((name, a, shared, q, nbytes))
 
     REPLAY_COPIES = 8
@@ -622,6 +630,9 @@ def bench_e2e(args):
         llm.generate(prompt_token_ids=warm_prompts, sampling_params=warm_sp)
         reset_prefix_cache()
         _log("e2e: warmup generate done")
+    # 32 sampled steps x (28 queries of up to 256 x 16 x 128 bf16 + tables
+    # of the graphs' 2560-block width): ~1 GiB, allocated before timing
+    probe["arena"] = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
     probe["on"] = True
     hits0 = eng.prefix_cache.hit_tokens
@@ -649,6 +660,7 @@ def bench_e2e(args):
         gdurs, gbytes = replay_saved()
     probe["saved"].clear()
     probe["shared"].clear()
+    probe["arena"] = None
     cpu_state = cpu_cfg = None
     by_prompt = {tuple(o.prompt_token_ids): list(o.output_token_ids) for o in outs}
     streams = [by_prompt[tuple(p)] for p in prompts[:8]]
