@@ -315,11 +315,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(
 // together.  A wavefront streams its whole range without draining: when the
 // next block belongs to another sequence it finishes the current one and
 // starts the next.  A sequence lying entirely inside one range is written
-// straight to `out`; only the first and last piece of a range can be partial
-// (slot 0 / slot 1 of that workgroup), and attn_persist_reduce_kernel merges
-// the pieces of sequences that span several ranges (the kernel boundary
-// orders the partial writes before their reads without any device-scope
-// fence inside the streaming kernel).
+// straight to `out`; only the first and last piece of a range can be
+// partial.  Those pieces go to workspace slots (piece_slot: the first two
+// pieces of a sequence row-indexed), workgroup 0 writes one header word per
+// sequence (row_header), and attn_persist_reduce_kernel merges the pieces of
+// sequences that span several ranges (the kernel boundary orders the partial
+// writes before their reads without any device-scope fence inside the
+// streaming kernel).
 // ---------------------------------------------------------------------------
 // Shared-prefix (cascade) pass.  Decode sequences whose block tables begin
 // with the same physical blocks (prefix-cache hits) form a group; the
@@ -937,11 +939,17 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
   const int grid = (int)gridDim.x;
 
   const RangeSplit rs = make_range_split(total, grid);
-  // ws_off: offsets [num_seqs + 1], then each sequence's skipped blocks
+  // ws_off: offsets [num_seqs + 1], each sequence's skipped blocks
+  // [num_seqs], then its header word [num_seqs]
   if (blockIdx.x == 0)
     for (int i = threadIdx.x; i <= num_seqs; i += blockDim.x) {
       ws_off[i] = s_off[i];
-      if (has_pfx && i < num_seqs) ws_off[num_seqs + 1 + i] = s_skip[i];
+      if (i < num_seqs) {
+        const int skip = has_pfx ? s_skip[i] : 0;
+        if (has_pfx) ws_off[num_seqs + 1 + i] = skip;
+        const int nsplit = (skip * BS + kPrefixKeysPerSplit - 1) / kPrefixKeysPerSplit;
+        ws_off[2 * num_seqs + 1 + i] = row_header(s_off[i], s_off[i + 1], rs, nsplit);
+      }
     }
   if (total == 0) return;
   const int r0 = rs.start((int)blockIdx.x);
@@ -967,8 +975,8 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
 
   // Finish sequence sq: a piece covering the whole sequence goes straight
   // to `out` (merged with the row's shared-prefix partials, which the
-  // prefix launch before this one wrote), any other piece to this
-  // workgroup's slot 0 (first piece) or 1 (last), for the reduce kernel.
+  // prefix launch before this one wrote), any other piece to its workspace
+  // slot (piece_slot), for the reduce kernel.
   auto finish = [&](int sq) __attribute__((always_inline)) {
     st.merge_token_groups();
     const int a = s_off[sq], b = s_off[sq + 1];
@@ -1064,8 +1072,9 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
 #pragma unroll
         for (int j = 0; j < VEC; ++j) elem<T>::store(op + j, st.acc[g][j] * inv);
       } else {
-        const int slot = (a <= r0) ? 0 : 1;
-        const int64_t base = ((int64_t)blockIdx.x * 2 + slot) * H + hq;
+        const int slot = piece_slot(sq, rs.piece_rank(a, (int)blockIdx.x), (int)blockIdx.x,
+                                    num_seqs);
+        const int64_t base = (int64_t)slot * H + hq;
         float* wp = ws_acc + base * D + st.dc * VEC;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) wp[j] = st.acc[g][j] * inv;
@@ -1164,109 +1173,125 @@ __global__ __launch_bounds__(kPersistMaxWaves * 64) void attn_decode_persistent_
 // (same flattened split as the persistent kernel), together with its
 // shared-prefix partials if it has any; write zeros for a sequence with no
 // tokens.  Partials are merged in a fixed order: walked pieces in range
-// order, then prefix splits in key order.
+// order, then prefix splits in key order.  Thread = (query head, 4 dims).
 template <typename T, int D>
 __global__ __launch_bounds__(512) void attn_persist_reduce_kernel(
     const int32_t* __restrict__ ws_off, int num_seqs, int num_wgs, int num_heads,
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     T* __restrict__ out, int64_t out_stride, PrefixArgs pfx, int block_size) {
-  // workgroup = (sequence, 512 / D query heads); thread = (head, dim)
-  constexpr int HPW = 512 / D;
+  constexpr int LPH = D / 4;          // lanes per query head
+  constexpr int HPW = 512 / LPH;      // query heads per workgroup
   const int sq = blockIdx.x;
-  const int hq = blockIdx.y * HPW + (int)threadIdx.x / D;
-  const int d = (int)threadIdx.x % D;
+  const int hq = blockIdx.y * HPW + (int)threadIdx.x / LPH;
+  const int d = ((int)threadIdx.x % LPH) * 4;
   if (hq >= num_heads) return;
-  const int a = ws_off[sq], b = ws_off[sq + 1];
-  const RangeSplit rs = make_range_split(ws_off[num_seqs], num_wgs);
   T* op = out + (int64_t)sq * out_stride + (int64_t)hq * D + d;
-  // blocks of this sequence attended by the shared-prefix pass, and its splits
-  const int skip = pfx.blocks ? ws_off[num_seqs + 1 + sq] : 0;
-  const int nsplit = (skip * block_size + kPrefixKeysPerSplit - 1) / kPrefixKeysPerSplit;
   const int64_t pb = ((int64_t)sq * num_heads + hq) * kPrefixMaxSplits;
-  int g0 = 0, np = 0;          // walked pieces: ranges g0 .. g0 + np - 1
-  if (a != b) {
-    g0 = rs.owner(a);
-    const int g1 = rs.owner(b - 1);
-    if (g0 == g1) return;      // finished (with its prefix) by the decode kernel
-    np = g1 - g0 + 1;
-  } else if (nsplit == 0) {
-    elem<T>::store(op, 0.0f);
-    return;
+  // The header word and both row-indexed pieces are loaded together,
+  // whether or not the row needs the pieces (their slots always exist); the
+  // header then says which of them count and which prefix splits to load.
+  const int hdr = ws_off[2 * num_seqs + 1 + sq];
+  float2 pml[2], qml[4];
+  float4 pa[2], qa[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t base = ((int64_t)sq * 2 + i) * num_heads + hq;
+    pml[i] = *reinterpret_cast<const float2*>(ws_ml + base * 2);
+    pa[i] = *reinterpret_cast<const float4*>(ws_acc + base * D + d);
   }
-  // (m, l, acc[d]) of walked piece i
-  auto piece = [&](int i, float& m, float& l, float& v) {
-    const int g = g0 + i;
-    const int slot = (a <= rs.start(g)) ? 0 : 1;
-    const int64_t base = ((int64_t)g * 2 + slot) * num_heads + hq;
-    m = ws_ml[base * 2];
-    l = ws_ml[base * 2 + 1];
-    v = ws_acc[base * D + d];
+  int np = header_pieces(hdr);
+  const int nsplit = header_splits(hdr);
+  const bool need_pfx = pfx.blocks != nullptr && np != 1;
+#pragma unroll
+  for (int sp = 0; sp < 4; ++sp) {
+    qml[sp] = make_float2(kNegBig, 0.0f);
+    qa[sp] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (need_pfx && sp < nsplit) {
+      qml[sp] = *reinterpret_cast<const float2*>(pfx.ml + (pb + sp) * 2);
+      qa[sp] = *reinterpret_cast<const float4*>(pfx.acc + (pb + sp) * D + d);
+    }
+  }
+  // keep every load above the branches below
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    asm volatile("" ::"v"(pml[i].x), "v"(pml[i].y), "v"(pa[i].x), "v"(pa[i].y), "v"(pa[i].z),
+                 "v"(pa[i].w));
+#pragma unroll
+  for (int sp = 0; sp < 4; ++sp)
+    asm volatile("" ::"v"(qml[sp].x), "v"(qml[sp].y), "v"(qa[sp].x), "v"(qa[sp].y),
+                 "v"(qa[sp].z), "v"(qa[sp].w));
+  if (np == 1) return;     // finished (with its prefix) by the decode kernel
+  auto put = [&](float l, const float o[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) elem<T>::store(op + j, l > 0.0f ? o[j] / l : 0.0f);
   };
   if (np <= 2 && nsplit <= 4) {
-    // At most two pieces and four prefix splits (the common case): every
-    // value is loaded in one round trip, then merged in the order of the
-    // general loop below (same operations, same results).
-    float pm[2], pl[2], pa[2], qm[4], ql[4], qa[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      pm[i] = kNegBig; pl[i] = 0.0f; pa[i] = 0.0f;
-      if (i < np) piece(i, pm[i], pl[i], pa[i]);
-    }
-#pragma unroll
-    for (int sp = 0; sp < 4; ++sp) {
-      qm[sp] = kNegBig; ql[sp] = 0.0f; qa[sp] = 0.0f;
-      if (sp < nsplit) {
-        qm[sp] = pfx.ml[(pb + sp) * 2];
-        ql[sp] = pfx.ml[(pb + sp) * 2 + 1];
-        qa[sp] = pfx.acc[(pb + sp) * D + d];
-      }
-    }
+    // at most two pieces and four prefix splits (the common case): merged
+    // from the registers, in the order of the general loop below
     float M = kNegBig;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      if (i < np) M = fmaxf(M, pm[i]);
+      if (i < np) M = fmaxf(M, pml[i].x);
 #pragma unroll
     for (int sp = 0; sp < 4; ++sp)
-      if (sp < nsplit) M = fmaxf(M, qm[sp]);
-    float L = 0.0f, O = 0.0f;
+      if (sp < nsplit) M = fmaxf(M, qml[sp].x);
+    float L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       if (i < np) {
-        const float f = pl[i] * fast_exp2(pm[i] - M);
+        const float f = pml[i].y * fast_exp2(pml[i].x - M);
         L += f;
-        O = fmaf(pa[i], f, O);
+        O[0] = fmaf(pa[i].x, f, O[0]); O[1] = fmaf(pa[i].y, f, O[1]);
+        O[2] = fmaf(pa[i].z, f, O[2]); O[3] = fmaf(pa[i].w, f, O[3]);
       }
 #pragma unroll
     for (int sp = 0; sp < 4; ++sp)
       if (sp < nsplit) {
-        const float f = ql[sp] * fast_exp2(qm[sp] - M);
+        const float f = qml[sp].y * fast_exp2(qml[sp].x - M);
         L += f;
-        O = fmaf(qa[sp], f, O);
+        O[0] = fmaf(qa[sp].x, f, O[0]); O[1] = fmaf(qa[sp].y, f, O[1]);
+        O[2] = fmaf(qa[sp].z, f, O[2]); O[3] = fmaf(qa[sp].w, f, O[3]);
       }
-    elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
+    put(L, O);
     return;
   }
+  // three or more pieces, or more than four splits: pieces from their slots
+  int g0 = 0;
+  if (np == 3) {
+    const int a = ws_off[sq], b = ws_off[sq + 1];
+    const RangeSplit rs = make_range_split(ws_off[num_seqs], num_wgs);
+    g0 = rs.owner(a);
+    np = rs.owner(b - 1) - g0 + 1;
+  }
+  auto piece = [&](int i, float2& ml, float4& v) __attribute__((always_inline)) {
+    const int64_t base = (int64_t)piece_slot(sq, min(i, 2), g0 + i, num_seqs) * num_heads + hq;
+    ml = *reinterpret_cast<const float2*>(ws_ml + base * 2);
+    v = *reinterpret_cast<const float4*>(ws_acc + base * D + d);
+  };
   float M = kNegBig;
   for (int i = 0; i < np; ++i) {
-    float m, l, v;
-    piece(i, m, l, v);
-    M = fmaxf(M, m);
+    float2 ml; float4 v;
+    piece(i, ml, v);
+    M = fmaxf(M, ml.x);
   }
   for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, pfx.ml[(pb + sp) * 2]);
-  float L = 0.0f, O = 0.0f;
+  float L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int i = 0; i < np; ++i) {
-    float m, l, v;
-    piece(i, m, l, v);
-    const float f = l * fast_exp2(m - M);
+    float2 ml; float4 v;
+    piece(i, ml, v);
+    const float f = ml.y * fast_exp2(ml.x - M);
     L += f;
-    O = fmaf(v, f, O);
+    O[0] = fmaf(v.x, f, O[0]); O[1] = fmaf(v.y, f, O[1]);
+    O[2] = fmaf(v.z, f, O[2]); O[3] = fmaf(v.w, f, O[3]);
   }
   for (int sp = 0; sp < nsplit; ++sp) {
     const float f = pfx.ml[(pb + sp) * 2 + 1] * fast_exp2(pfx.ml[(pb + sp) * 2] - M);
     L += f;
-    O = fmaf(pfx.acc[(pb + sp) * D + d], f, O);
+    const float4 v = *reinterpret_cast<const float4*>(pfx.acc + (pb + sp) * D + d);
+    O[0] = fmaf(v.x, f, O[0]); O[1] = fmaf(v.y, f, O[1]);
+    O[2] = fmaf(v.z, f, O[2]); O[3] = fmaf(v.w, f, O[3]);
   }
-  elem<T>::store(op, L > 0.0f ? O / L : 0.0f);
+  put(L, O);
 }
 
 // Merge the partitions of one (row, query head); rows with a single
@@ -1360,10 +1385,13 @@ static AttnPlan plan_decode(int num_decodes, int num_heads, int num_kv_heads, in
     int pow2 = 2;
     while (pow2 < sync && pow2 < 64) pow2 *= 2;
     p.sync_mask = sync > 0 ? pow2 - 1 : -1;
-    // block offsets [num_decodes + 1] and shared-prefix skips [num_decodes]
-    p.off_bytes = align256(sizeof(int32_t) * (size_t)(2 * num_decodes + 1));
-    p.ml_bytes = align256(sizeof(float) * 2 * (size_t)p.num_wgs * 2 * num_heads);
-    p.acc_bytes = align256(sizeof(float) * (size_t)p.num_wgs * 2 * num_heads * head_dim);
+    // block offsets [num_decodes + 1], shared-prefix skips and header words
+    // [num_decodes] each; piece slots (piece_slot): two per decode row and
+    // one per workgroup, each (m, l) and head_dim floats per query head
+    const size_t slots = 2 * (size_t)num_decodes + (size_t)p.num_wgs;
+    p.off_bytes = align256(sizeof(int32_t) * (size_t)(3 * num_decodes + 1));
+    p.ml_bytes = align256(sizeof(float) * 2 * slots * num_heads);
+    p.acc_bytes = align256(sizeof(float) * slots * num_heads * head_dim);
     return p;
   }
   const int unit = kAttnWaves * block_size;
@@ -1425,7 +1453,7 @@ static void launch_persistent(const void* q, int64_t q_stride, const void* kc, c
                      dim3(64 * num_kv_heads), lds, st, (const T*)q, q_stride, (const T*)kc,
                      (const T*)vc, num_kv_heads, num_cache_blocks, bt, max_blocks, ctx, num_seqs,
                      scale_log2, (T*)out, out_stride, ws_off, ws_acc, ws_ml, pfx, p.sync_mask);
-  constexpr int kHeadsPerReduceWg = 512 / D;
+  constexpr int kHeadsPerReduceWg = 512 / (D / 4);
   const int H = num_kv_heads * G;
   hipLaunchKernelGGL((attn_persist_reduce_kernel<T, D>),
                      dim3(num_seqs, (H + kHeadsPerReduceWg - 1) / kHeadsPerReduceWg), dim3(512),

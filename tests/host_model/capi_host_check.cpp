@@ -2,9 +2,10 @@
 // with no GPU: the library's sources are compiled host-only (no device code)
 // and linked into this driver by tests/test_host_model.py.  It checks
 //   * every workspace-size function against a model of what the kernels
-//     address (the persistent decode kernel: block offsets and shared-prefix
-//     skips [2B + 1] ints, two boundary slots per workgroup of (m, l) and
-//     D floats per query head, at up to 4 x the CU count workgroups; the
+//     address (the persistent decode kernel: block offsets, shared-prefix
+//     skips and header words [3B + 1] ints, piece slots -- two per row and
+//     one per workgroup -- of (m, l) and D floats per query head, at up to
+//     4 x the CU count workgroups; the
 //     per-row kernel: one partial per 256-token partition; the prefix pass:
 //     16 splits of (m, l) + D floats per row and head; the sampler: a
 //     (maximum, sigma) pair per (row, 512-element segment)), over
@@ -39,8 +40,9 @@ static size_t a256(size_t x) { return (x + 255) / 256 * 256; }
 static size_t decode_need(int B, int H, int D, int bs, int max_blocks, int cus) {
   // persistent kernel, worst case one kv head: 4 workgroups per CU
   const size_t wgs = (size_t)cus * 4;
-  const size_t pers = a256(4 * (size_t)(2 * B + 1)) + a256(4 * 2 * wgs * 2 * H) +
-                      a256(4 * wgs * 2 * H * D);
+  const size_t slots = 2 * (size_t)B + wgs;
+  const size_t pers = a256(4 * (size_t)(3 * B + 1)) + a256(4 * 2 * slots * H) +
+                      a256(4 * slots * H * D);
   // workgroup-per-row kernel (above 8 kv heads): 256-token partitions
   const size_t unit = 4 * (size_t)bs;
   const size_t part = (256 + unit - 1) / unit * unit;

@@ -5,12 +5,15 @@
 //   * the ranges [start(b), start(b+1)) partition [0, total) for every grid
 //     size, and owner(p) is the range holding p, for every p;
 //   * the piece bookkeeping of the decode kernel and its reduce kernel
-//     agree: every row's pieces are written once each, into workgroup
-//     slots 0 / 1 that no other row of that workgroup uses, and the reduce
-//     kernel reads exactly those (same workgroup, same slot), for random
-//     ragged rows with and without walked blocks;
+//     agree: every row's pieces are written once each, into slots
+//     (piece_slot: pieces 0 / 1 row-indexed, later ones in their
+//     workgroup's slot) that no other row uses, the header word
+//     (row_header) carries the row's piece count and prefix splits, and the
+//     reduce kernel reads exactly the written slots (from the header alone
+//     for up to two pieces, from the offsets beyond), for random ragged rows
+//     with and without walked blocks;
 //   * every slot index stays inside the workspace the host sizes for it
-//     (2 slots per workgroup).
+//     (2 slots per row + 1 per workgroup).
 // Exit status 0 = all checks passed; a message and status 1 otherwise.
 #include <cstdio>
 #include <cstdlib>
@@ -48,14 +51,15 @@ static void check_split(int total, int grid) {
 }
 
 // Decode kernel / reduce kernel piece bookkeeping for one batch.
-static void check_pieces(const std::vector<int>& walked, int grid) {
+static void check_pieces(const std::vector<int>& walked, int grid, std::mt19937& rng) {
   const int n = (int)walked.size();
   std::vector<int> off(n + 1, 0);
   for (int i = 0; i < n; ++i) off[i + 1] = off[i] + walked[i];
   const int total = off[n];
   const lv::RangeSplit r = lv::make_range_split(total, grid);
-  std::map<std::pair<int, int>, int> slot_owner;            // (workgroup, slot) -> row
-  std::map<int, std::set<std::pair<int, int>>> pieces;      // row -> its slots
+  const int num_slots = 2 * n + grid;
+  std::map<int, int> slot_owner;                 // slot -> row
+  std::map<int, std::set<int>> pieces;           // row -> its slots
   std::vector<int> whole_by(n, -1);
   for (int g = 0; g < grid; ++g) {
     const int r0 = r.start(g), r1 = r.start(g + 1);
@@ -68,31 +72,44 @@ static void check_pieces(const std::vector<int>& walked, int grid) {
         whole_by[sq] = g;
         continue;
       }
-      const int slot = (a <= r0) ? 0 : 1;
-      CHECK(slot >= 0 && slot < 2 && g < grid, "slot index outside the workspace");
-      const auto key = std::make_pair(g, slot);
-      CHECK(!slot_owner.count(key), "workgroup %d slot %d written by two rows (%d)", g, slot, sq);
-      slot_owner[key] = sq;
-      pieces[sq].insert(key);
+      const int rank = r.piece_rank(a, g);
+      const int exact = g - r.owner(a);
+      CHECK(rank == (exact < 2 ? exact : 2), "row %d piece %d: rank %d", sq, exact, rank);
+      const int slot = lv::piece_slot(sq, rank, g, n);
+      CHECK(slot >= 0 && slot < num_slots, "slot %d outside the workspace (%d)", slot, num_slots);
+      CHECK(!slot_owner.count(slot), "slot %d written by rows %d and %d", slot, slot_owner[slot],
+            sq);
+      slot_owner[slot] = sq;
+      pieces[sq].insert(slot);
     }
   }
   for (int sq = 0; sq < n; ++sq) {
     const int a = off[sq], b = off[sq + 1];
+    const int nsplit = (int)(rng() % 17);
+    const int h = lv::row_header(a, b, r, nsplit);
+    CHECK(lv::header_splits(h) == nsplit, "row %d: header splits", sq);
+    const int np = lv::header_pieces(h);
     if (a == b) {
-      CHECK(!pieces.count(sq) && whole_by[sq] < 0, "empty row %d has pieces", sq);
+      CHECK(np == 0 && !pieces.count(sq) && whole_by[sq] < 0, "empty row %d", sq);
       continue;
     }
-    const int g0 = r.owner(a), g1 = r.owner(b - 1);
-    if (g0 == g1) {
-      CHECK(whole_by[sq] == g0 && !pieces.count(sq), "row %d: reduce sees whole in %d, kernel %d",
-            sq, g0, whole_by[sq]);
+    if (np == 1) {
+      CHECK(whole_by[sq] == r.owner(a) && !pieces.count(sq), "row %d: header says whole", sq);
       continue;
     }
-    std::set<std::pair<int, int>> read;
-    for (int g = g0; g <= g1; ++g) read.insert({g, (a <= r.start(g)) ? 0 : 1});
-    CHECK(read == pieces[sq], "row %d: reduce reads %zu pieces, kernel wrote %zu", sq,
+    CHECK(np == 2 || np == 3, "row %d: header pieces %d", sq, np);
+    std::set<int> read;
+    if (np == 2) {
+      read = {2 * sq, 2 * sq + 1};               // the reduce kernel's fast path
+      CHECK(r.owner(b - 1) - r.owner(a) == 1, "row %d: two pieces", sq);
+    } else {
+      const int g0 = r.owner(a), cnt = r.owner(b - 1) - g0 + 1;
+      CHECK(cnt >= 3, "row %d: header 3, %d pieces", sq, cnt);
+      for (int i = 0; i < cnt; ++i) read.insert(lv::piece_slot(sq, i < 2 ? i : 2, g0 + i, n));
+    }
+    CHECK(read == pieces[sq], "row %d: reduce reads %zu slots, kernel wrote %zu", sq,
           read.size(), pieces[sq].size());
-    for (const auto& k : read)
+    for (int k : read)
       CHECK(slot_owner.count(k) && slot_owner[k] == sq, "row %d reads a slot of another row", sq);
   }
 }
@@ -108,7 +125,7 @@ int main() {
     std::vector<int> walked(n);
     const int maxb = 1 + (int)(rng() % 200);
     for (int& w : walked) w = (rng() % 7 == 0) ? 0 : (int)(rng() % maxb);
-    check_pieces(walked, grids[rng() % 10]);
+    check_pieces(walked, grids[rng() % 10], rng);
   }
   if (g_fail) {
     std::fprintf(stderr, "%d checks failed\n", g_fail);
