@@ -444,6 +444,20 @@ template <int D, int W> struct ChunkLds {
 };
 
 
+// max / sum of x over lanes l and l ^ 32 (v_permlane32_swap: lanes 0-31 of
+// one copy trade places with lanes 32-63 of the other, so each lane holds
+// its own value and its partner's), no LDS round trip.
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ i16x4_t lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)p);
 }
@@ -716,7 +730,7 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[kb][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+    mx = xor32_max(mx) * scale_log2;
     float alpha = 1.0f;
     if (mx > m_run + 8.0f) {
       alpha = fast_exp2(m_run - mx);
@@ -833,7 +847,7 @@ __device__ __forceinline__ void chunk_mfma_body(const ChunkArgs<T>& A, int unit,
 
   // Row sum over both halves of the wavefront, then write this lane's
   // query row: O^T slot i of block b is dim 32 b + 8 (i / 4) + 4 h + i % 4.
-  l_run += __shfl_xor(l_run, 32);
+  l_run = xor32_sum(l_run);
   if (qtok >= qlen || !qrow_ok) return;
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
   if constexpr (PFX) {
