@@ -1192,7 +1192,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(512) void attn_persist_reduce_kernel(
     const int32_t* __restrict__ ws_off, int num_seqs, int num_wgs, int num_heads,
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
-    T* __restrict__ out, int64_t out_stride, PrefixArgs pfx, int block_size) {
+    T* __restrict__ out, int64_t out_stride, PrefixArgs pfx) {
   constexpr int LPH = D / 4;          // lanes per query head
   constexpr int HPW = 512 / LPH;      // query heads per workgroup
   const int sq = blockIdx.x;
@@ -1472,7 +1472,7 @@ static void launch_persistent(const void* q, int64_t q_stride, const void* kc, c
   hipLaunchKernelGGL((attn_persist_reduce_kernel<T, D>),
                      dim3(num_seqs, (H + kHeadsPerReduceWg - 1) / kHeadsPerReduceWg), dim3(512),
                      0, st, (const int32_t*)ws_off, num_seqs, p.num_wgs, H,
-                     (const float*)ws_acc, (const float*)ws_ml, (T*)out, out_stride, pfx, BS);
+                     (const float*)ws_acc, (const float*)ws_ml, (T*)out, out_stride, pfx);
 }
 
 // Everything one launch needs besides the dtype / shape template arguments.
