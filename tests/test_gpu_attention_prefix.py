@@ -118,6 +118,25 @@ def test_prefix_covers_whole_context(device):
     _check(_run(b, device, plan), _oracle(b), "whole-context prefix")
 
 
+def test_prefix_long_rows_many_pieces(device):
+    """Long rows (each spread over many workgroup ranges) with a shared
+    prefix of more than four 128-key splits, rows whose whole context is
+    that prefix, a row with one block past it, and long rows without a
+    prefix: the reduce kernel's general merge (pieces from their slots,
+    splits in a loop) for every combination."""
+    _say("prefix long rows, many pieces and splits")
+    b = workloads.paged_decode(seed=17, num_seqs=12, ctx_lo=5000, ctx_hi=9000,
+                               scale_inputs=False,
+                               ctx_head=[1024, 1024, 7000, 9000, 1030, 6000])
+    groups = [(list(range(0, 6)), 64), ([6, 7, 8], 20)]
+    b = _share(b, groups)
+    plan = ops.prefix_plan(groups, b.num_decodes, 2, device)
+    got = _run(b, device, plan)
+    _check(got, _oracle(b), "long rows with prefix")
+    plain = _run(b, device)
+    assert (got.float() - plain.float()).abs().max() <= 2e-2
+
+
 def test_prefix_padding_and_workspace_reuse(device):
     """A padded plan (unused items) and back-to-back calls with different
     plans on the same workspaces: stale partials are never read."""
