@@ -191,14 +191,17 @@ def test_decode_lockstep_interval_bit_identical(device, heads, monkeypatch):
 
 @pytest.mark.parametrize("knobs", [
     {"LV_ATTN_NBUF": "4"}, {"LV_ATTN_NT": "0"}, {"LV_ATTN_PERSIST_WGS": "97"},
+    {"LV_ATTN_PERSIST_WGS": "1"}, {"LV_ATTN_PERSIST_WGS": "1024"},
     {"LV_ATTN_DECODE_KERNEL": "rows"},
     {"LV_ATTN_DECODE_KERNEL": "rows", "LV_ATTN_PART_TOKENS": "128"},
     {"LV_ATTN_CHUNK_KERNEL": "rows"}])
 def test_attention_tuning_knobs(device, knobs, monkeypatch):
     """The per-call tuning knobs of lv_paged_attention (register buffers,
-    load type, persistent grid, the fallback row kernels and their partition
-    size) keep a mixed step within the attention bar; the two that change
-    only prefetch depth or load type leave it bit-identical."""
+    load type, persistent grid -- one workgroup: every row whole; 1024: the
+    40 rows cut into ranges of a few blocks, most rows in three or more
+    pieces -- the fallback row kernels and their partition size) keep a
+    mixed step within the attention bar; the two that change only prefetch
+    depth or load type leave it bit-identical."""
     _say(f"attention knobs {knobs}")
     step = workloads.mixed_step(seed=13, num_decodes=40, dec_lo=1, dec_hi=2500, num_chunks=3,
                                 chunk_len=90, off_hi=700, num_cache_slots=16 * 3000)
